@@ -1,0 +1,400 @@
+"""Benchmark: encoder images/sec @256x256 fp16 on one MI355X, with per-op
+roofline fractions and the CPU oracle timed beside it.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-suite]
+
+A step is one whole-plan replay -- the 259-op ViT encoder (BASELINE cfg 4:
+12 blocks, hidden 768, 12 heads, MLP 3072, LayerNorm, 2D RoPE, merger) over one
+256x256 image, replayed as ONE captured hipGraph through the session's batch
+invoke. Inputs and weights are resident in HBM before timing starts. `value`
+is images/sec over exactly K replays bracketed by device synchronisation.
+
+Per-op durations come from the same product path: a blob that repeats one op
+R times, captured as a hipGraph and timed with HIP events on the session
+stream (cycles_total of a TIMED invoke), divided by R. "in_plan" figures use
+the plan's own buffers (cache-warm, as in the encoder); the "suite" figures
+rotate R distinct buffer sets whose footprint exceeds 512 MB (above the
+256 MB MALL), so they measure HBM, at BASELINE cfg 2/3 shapes.
+
+Roofline peaks: HBM 8 TB/s; dense fp16 MFMA 2.5 PFLOP/s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from dataclasses import replace
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+METRIC = "encoder images/sec @256x256 fp16, 1 GPU; per-op % of MFMA/HBM roofline"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---- algorithmic work per op --------------------------------------------------------
+
+_ESZ = {"fp16": 2, "fp32": 4}
+
+
+def op_work(spec_name: str, in_shapes, out_shape, in_dtypes, out_dtype) -> tuple[str, float]:
+    """('mfma', flops) for GEMMs, ('hbm', bytes) for everything else: every
+    input read once and every output written once."""
+    def nb(shape, dt):
+        n = int(np.prod(shape))
+        return n // 32 * 18 if dt == "q4_0" else n * _ESZ[dt]
+    if spec_name == "matmul":
+        bn, m, k = in_shapes[0]
+        n = in_shapes[1][-1]
+        return "mfma", 2.0 * bn * m * k * n
+    if spec_name.startswith("matmul_epilogue"):
+        m, k = in_shapes[0]
+        n = in_shapes[1][-1]
+        return "mfma", 2.0 * m * k * n
+    total = sum(nb(s, d) for s, d in zip(in_shapes, in_dtypes)) + nb(out_shape, out_dtype)
+    return "hbm", float(total)
+
+
+def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
+    def nb(shape, dt):
+        n = int(np.prod(shape))
+        return n // 32 * 18 if dt == "q4_0" else n * _ESZ[dt]
+    return sum(nb(s, d) for s, d in zip(in_shapes, in_dtypes)) + nb(out_shape, "fp16")
+
+
+# ---- plan helpers -------------------------------------------------------------------------
+
+def build_plan(cfg, seed=0, weight_layout=None):
+    from hexlib_amd import encoder as E
+    from hexlib_amd.exec.wholeplan import build_whole_plan_batch
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg, seed=seed)
+    return g, feeds, build_whole_plan_batch(g, feeds, weight_layout=weight_layout)
+
+
+def time_replays(plan, steps: int, warmup: int) -> float:
+    """Seconds for exactly `steps` graph replays, bracketed by device syncs."""
+    import torch
+    from hexlib_amd import lib as L
+    flags = L.INVOKE_GRAPH | L.INVOKE_NOSYNC
+    kinds = plan.kinds
+    for _ in range(max(warmup, 1)):
+        plan.session.invoke(plan.batch.blob, kinds, flags)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        plan.session.invoke(plan.batch.blob, kinds, flags)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def unique_ops(g, wb):
+    """(spec, input shapes/dtypes, output) -> [count, first op desc index]."""
+    from hexlib_amd.graph.fuse import fuse
+    f = fuse(g)
+    out = {}
+    i = 0
+    for op in f.ops:
+        if op.kind == "reshape":
+            continue
+        spec = wb.op_specs[i]
+        ins = tuple((wb.placements[n].shape, wb.placements[n].dtype) for n in op.inputs)
+        o = wb.placements[op.outputs[0]]
+        key = (spec, ins, (o.shape, o.dtype))
+        if key not in out:
+            out[key] = [0, i, op]
+        out[key][0] += 1
+        i += 1
+    return out
+
+
+def repeat_op_blob(wb, op_index: int, reps: int) -> bytes:
+    """The plan's blob with its op list replaced by `reps` copies of one op."""
+    import struct
+    from hexlib_amd.exec import wire
+    blob = wb.blob
+    hdr = list(struct.unpack_from(wire._HDR, blob))
+    off_ops = hdr[8]
+    op = blob[off_ops + op_index * wire.OP_SIZE: off_ops + (op_index + 1) * wire.OP_SIZE]
+    body = bytearray(blob[:off_ops] + op * reps)
+    struct.pack_into("<I", body, 8, len(body))
+    struct.pack_into("<I", body, 20, reps)
+    return bytes(body)
+
+
+def time_blob(session, blob: bytes, n_ops: int, iters: int = 5) -> float:
+    """Mean GPU ns of one replay of a captured blob (TIMED graph invoke)."""
+    from hexlib_amd import lib as L
+    from hexlib_amd.exec.gpu import blob_kinds
+    kinds = blob_kinds(blob)
+    session.invoke(blob, kinds, L.INVOKE_GRAPH)             # capture + first run
+    ns = []
+    for _ in range(iters):
+        rsp = session.invoke(blob, kinds, L.INVOKE_GRAPH | L.INVOKE_TIMED)
+        ns.append(rsp.cycles_total)
+    return float(np.median(ns))
+
+
+def per_op_in_plan(plan, g, reps: int = 40) -> list[dict]:
+    rows = []
+    for (spec, ins, (oshape, odt)), (count, idx, op) in unique_ops(g, plan.batch).items():
+        blob = repeat_op_blob(plan.batch, idx, reps)
+        ns = time_blob(plan.session, blob, reps) / reps
+        bound, work = op_work(spec, [s for s, _ in ins], oshape, [d for _, d in ins], odt)
+        rate = work / ns  # flops/ns = GFLOP/s ; bytes/ns = GB/s
+        peak = MFMA_FP16_PEAK_TFLOPS * 1e3 if bound == "mfma" else HBM_PEAK_GBS
+        rows.append({"op": spec, "shape": [list(s) for s, _ in ins], "count": count,
+                     "avg_ns": round(ns, 1), "bound": bound,
+                     "achieved": round(rate / 1e3, 3) if bound == "mfma" else round(rate, 1),
+                     "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                     "frac": round(rate / peak, 4),
+                     "total_us": round(count * ns / 1e3, 1)})
+    return sorted(rows, key=lambda r: -r["total_us"])
+
+
+# ---- cold-buffer per-op suite (BASELINE cfg 2 / cfg 3 shapes) -------------------------
+
+def suite_cases():
+    from hexlib_amd import encoder as E
+    r = np.random.default_rng(0)
+    cos, sin = E.rope_tables(E.QWEN35_VISION_FP16)
+    h = lambda *s: (r.standard_normal(s)).astype(np.float16)
+    return [
+        ("rmsnorm", {"eps": 1e-6}, [h(256, 768), h(768)], (256, 768)),
+        ("layernorm", {"eps": 1e-6}, [h(256, 768), np.ones(768, np.float32), np.zeros(768, np.float32)], (256, 768)),
+        ("softmax", {"axis": -1}, [(h(12, 256, 256) * 0.125).astype(np.float16)], (12, 256, 256)),
+        ("rope_2d", {}, [h(256, 12, 64), cos, sin], (256, 12, 64)),
+        ("transpose", {"perm": (1, 0, 2)}, [h(256, 12, 64)], (12, 256, 64)),
+        ("transpose", {"perm": (0, 2, 1)}, [h(12, 256, 64)], (12, 64, 256)),
+        ("add", {}, [h(256, 768), h(256, 768)], (256, 768)),
+        ("scale", {"factor": 0.125}, [h(256, 768)], (256, 768)),
+        ("cast", {"dtype": "fp16"}, [r.standard_normal((256, 768)).astype(np.float32)], (256, 768)),
+        ("patchify", {"patch": 16, "temporal_patch": 1, "merge": 2, "grid_h": 16, "grid_w": 16},
+         [r.random((3, 1, 256, 256), dtype=np.float32)], (256, 768)),
+        ("matmul_epilogue", {"act": "gelu_tanh"}, [h(256, 768), (h(768, 2304) * 0.02).astype(np.float16),
+                                                   np.zeros(2304, np.float32)], (256, 2304)),
+        ("matmul_epilogue", {"act": "none"}, [h(256, 768), (h(768, 768) * 0.02).astype(np.float16),
+                                              np.zeros(768, np.float32)], (256, 768)),
+        ("matmul_epilogue", {"act": "gelu_tanh"}, [h(256, 768), (h(768, 3072) * 0.02).astype(np.float16),
+                                                   np.zeros(3072, np.float32)], (256, 3072)),
+        ("matmul_epilogue", {"act": "none"}, [h(256, 3072), (h(3072, 768) * 0.02).astype(np.float16),
+                                              np.zeros(768, np.float32)], (256, 768)),
+        ("matmul", {}, [h(12, 256, 64), h(12, 64, 256)], (12, 256, 256)),
+        ("matmul", {}, [h(12, 256, 256), h(12, 256, 64)], (12, 256, 64)),
+    ]
+
+
+def suite(session, min_footprint=600 << 20, max_reps=400) -> list[dict]:
+    import torch
+    from hexlib_amd.exec import wire
+    from hexlib_amd.exec.runner import KIND_ID, select
+    from hexlib_amd.exec.wholeplan import align_up
+    rows = []
+    fd = 11
+    for kind, attrs, arrays, out_shape in suite_cases():
+        dtypes = ["fp16" if a.dtype == np.float16 else "fp32" for a in arrays]
+        name, spec = select(kind, attrs, dtypes)
+        odt = spec.out_dtype
+        blobs = [np.ascontiguousarray(a).tobytes() for a in arrays]
+        onb = int(np.prod(out_shape)) * _ESZ[odt]
+        sizes = [align_up(len(b)) for b in blobs] + [align_up(onb)]
+        per = sum(sizes)
+        reps = int(min(max_reps, max(8, -(-min_footprint // per))))
+        reps = min(reps, (wire.MAX_TENSORS - 1) // (len(arrays) + 1))
+        arena = torch.empty(per * reps, dtype=torch.uint8, device="cuda")
+        one = bytearray(per)
+        off = 0
+        for b, s in zip(blobs, sizes):
+            one[off:off + len(b)] = b
+            off += s
+        arena.view(reps, per).copy_(torch.frombuffer(one, dtype=torch.uint8).to("cuda").expand(reps, per))
+        torch.cuda.synchronize()
+        tensors, ops = [], []
+        shapes = [a.shape for a in arrays]
+        lays = spec.buf_layouts()
+        for r in range(reps):
+            base = r * per
+            idx = []
+            off = 0
+            for i, (a, s) in enumerate(zip(arrays, sizes[:-1])):
+                tensors.append(wire.TensorDesc(0, base + off, len(blobs[i]), dtypes[i], lays[i], wire.pad_ne(a.shape)))
+                idx.append(len(tensors) - 1)
+                off += s
+            tensors.append(wire.TensorDesc(0, base + off, onb, odt, lays[-1], wire.pad_ne(out_shape)))
+            ops.append(wire.OpDesc(KIND_ID[name], spec.params(shapes, attrs), tuple(idx), (len(tensors) - 1,)))
+        blob = wire.pack_batch([wire.BufDesc(fd, per * reps)], tensors, ops)
+        session.mmap(fd, arena.data_ptr(), per * reps)
+        try:
+            ns = time_blob(session, blob, reps) / reps
+        finally:
+            session.munmap(fd)
+        bound, work = op_work(name, shapes, out_shape, dtypes, odt)
+        rate = work / ns
+        peak = MFMA_FP16_PEAK_TFLOPS * 1e3 if bound == "mfma" else HBM_PEAK_GBS
+        row = {"op": name, "shape": [list(s) for s in shapes], "avg_ns": round(ns, 1), "bound": bound,
+               "achieved": round(rate / 1e3, 3) if bound == "mfma" else round(rate, 1),
+               "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "frac": round(rate / peak, 4),
+               "footprint_mb": round(per * reps / 2**20), "reps": reps}
+        if bound == "mfma":
+            gb = gemm_bytes(shapes, dtypes, out_shape)
+            attain = min(MFMA_FP16_PEAK_TFLOPS * 1e3, work / gb * HBM_PEAK_GBS)
+            row["frac_of_attainable"] = round(rate / attain, 4)
+        rows.append(row)
+        log(f"suite {name} {shapes}: {ns:.0f} ns, {row['achieved']} {row['unit']} ({row['frac']*100:.1f}%)")
+        del arena
+        torch.cuda.empty_cache()
+    return rows
+
+
+# ---- CPU baseline ------------------------------------------------------------------------
+
+def cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
+    from hexlib_amd import encoder as E
+    from hexlib_amd.graph.fuse import fuse
+    from oracle import eager
+    g = fuse(E.build_vision_encoder(cfg))
+    feeds = E.synthetic_feeds(g, cfg, seed=0)
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001 -- informational only
+        threads = os.cpu_count()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        eager.run_stored(g, feeds)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    return {"value": round(n / el, 4), "unit": "images/s", "cores": int(threads or 1),
+            "kind": "port",
+            "sample": f"{n} image(s) of the cfg-4 256x256 encoder through the numpy oracle "
+                      f"(storage-rounding interpreter restatement) in {el:.1f} s; "
+                      f"os.cpu_count()={os.cpu_count()}, numpy {np.__version__}"}
+
+
+# ---- main -------------------------------------------------------------------------------
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--no-variants", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested). Images are independent; see DESIGN.md "
+              f"for how the plan would shard.", file=sys.stderr)
+        return 2
+
+    import torch
+    from hexlib_amd import encoder as E
+    from hexlib_amd.exec.gpu import GpuPlan, GpuSession
+
+    session = GpuSession()
+    cfg = E.QWEN35_VISION_FP16
+    log("building cfg-4 plan (256x256, batch 1)")
+    g, feeds, wb = build_plan(cfg)
+    plan = GpuPlan(wb, session)
+    sec = time_replays(plan, args.steps, args.warmup)
+    ms = sec / args.steps * 1e3
+    ips = args.steps * cfg.batch / sec
+    log(f"encoder b1: {ms:.3f} ms/image, {ips:.1f} images/s")
+
+    log("per-op timing inside the plan")
+    per_op = per_op_in_plan(plan, g)
+    plan_gpu_ns = None
+    try:
+        from hexlib_amd import lib as L
+        rsp = session.invoke(wb.blob, plan.kinds, L.INVOKE_GRAPH | L.INVOKE_TIMED)
+        plan_gpu_ns = rsp.cycles_total
+    except Exception as e:  # noqa: BLE001
+        log(f"timed graph replay failed: {e}")
+    plan.close()
+
+    # dominant kernel by share of the plan's time
+    dom_spec = {}
+    for r in per_op:
+        d = dom_spec.setdefault(r["op"], {"ns": 0.0, "work": 0.0, "count": 0, "bound": r["bound"]})
+        d["ns"] += r["count"] * r["avg_ns"]
+        d["count"] += r["count"]
+        unit = 1e3 if r["bound"] == "mfma" else 1.0
+        d["work"] += r["count"] * r["avg_ns"] * r["achieved"] * unit
+    dom_name, dom = max(dom_spec.items(), key=lambda kv: kv[1]["ns"])
+    achieved = dom["work"] / dom["ns"]
+    if dom["bound"] == "mfma":
+        roof = {"kernel": dom_name, "bound": "mfma", "achieved": round(achieved / 1e3, 3),
+                "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / 1e3 / MFMA_FP16_PEAK_TFLOPS, 5)}
+    else:
+        roof = {"kernel": dom_name, "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5)}
+    roof.update({"traffic": None, "launches_per_image": dom["count"],
+                 "avg_launch_ns": round(dom["ns"] / dom["count"], 1),
+                 "share_of_plan": round(dom["ns"] / sum(v["ns"] for v in dom_spec.values()), 3)})
+
+    variants = {}
+    if not args.no_variants:
+        for label, vcfg, steps in (("256_b32", replace(cfg, batch=32), max(5, args.steps // 10)),
+                                   ("448_b1", E.encoder_at(448), max(10, args.steps // 2))):
+            log(f"variant {label}")
+            gv, _, wbv = build_plan(vcfg)
+            pv = GpuPlan(wbv, session)
+            s = time_replays(pv, steps, 3)
+            variants[label] = {"images_per_s": round(steps * vcfg.batch / s, 2),
+                               "ms_per_step": round(s / steps * 1e3, 3), "batch": vcfg.batch,
+                               "tokens": vcfg.num_tokens, "steps": steps}
+            if label == "256_b32":
+                rows = per_op_in_plan(pv, gv, reps=10)
+                mm = [r for r in rows if r["bound"] == "mfma"]
+                fl = sum(r["count"] * r["avg_ns"] * r["achieved"] * 1e3 for r in mm)
+                t = sum(r["count"] * r["avg_ns"] for r in mm)
+                variants[label]["gemm_tflops"] = round(fl / t / 1e3, 2) if t else None
+                variants[label]["gemm_frac_of_peak"] = round(fl / t / 1e3 / MFMA_FP16_PEAK_TFLOPS, 4) if t else None
+                variants[label]["per_op"] = rows
+            pv.close()
+            log(f"variant {label}: {variants[label]['images_per_s']} images/s")
+
+    suite_rows = [] if args.no_suite else suite(session)
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (numpy oracle)")
+        cpu = cpu_baseline(cfg)
+
+    line = {
+        "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: seeded U[0,1] image, N(0,0.02) fp16 weights, random init",
+        "config": {"workload": "vit_encoder_256_b1 (BASELINE cfg 4: 12 blocks, hidden 768, "
+                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; 259 ops as one hipGraph)",
+                   "image": 256, "batch": 1, "tokens": 256, "plan_gpu_ns": plan_gpu_ns},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "per_op_in_plan": per_op,
+        "per_op_suite_cold": suite_rows,
+        "variants": variants,
+    }
+    session.close()
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

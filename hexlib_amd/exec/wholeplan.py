@@ -1,0 +1,216 @@
+"""A whole encoder plan as ONE batch blob over ONE device arena.
+
+Restates `build_whole_plan_batch` (`hexlib/exec/wholeplan.py:92-357`): every
+tensor lives in a single buffer (fd 0) split into regions --
+
+  const  every weight, bias and table, each at its own offset;
+  act    every activation at its own offset (no liveness reuse: HBM is 288 GB,
+         and a non-aliased arena is the configuration the reference runs by
+         default, `alias_activations=False`);
+  io     the graph input and output.
+
+A reshape emits no op: its output is placed at its input's offset with its own
+extents. The variant for each op is chosen on the host (`runner.select`) from
+its attrs and input dtypes, and each tensor's bytes take the dtype and layout
+the consuming spec declares (the fp32 pos_embed is staged as fp16; a q4_0
+weight is quantized here, blocked along N or grouped along K per the chosen
+layout). Offsets are 256-byte aligned so every kernel's vector path applies.
+
+The plan order is the fused graph's op order (a valid topological order; with
+no aliasing the result does not depend on which one).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Mapping
+
+import numpy as np
+
+from hexlib_amd.exec import wire
+from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, RunnerSpec, select
+from hexlib_amd.graph.fuse import fuse
+from hexlib_amd.graph.ir import Graph
+from hexlib_amd.graph.ir import nbytes as ir_nbytes
+from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
+
+ALIGN = 256
+_NP = {"fp32": np.float32, "fp16": np.float16, "int32": np.int32}
+
+
+class WholePlanError(Exception):
+    pass
+
+
+def align_up(n: int, a: int = ALIGN) -> int:
+    return (n + a - 1) // a * a
+
+
+@dataclass(frozen=True)
+class Placement:
+    name: str
+    offset: int
+    nbytes: int
+    dtype: str
+    layout: str
+    ne: tuple[int, int, int, int]
+    region: str  # const | act | io | reshape-alias
+    shape: tuple[int, ...] = ()
+
+
+@dataclass
+class WholePlanBatch:
+    blob: bytes
+    payload: bytearray            # initial arena contents (consts + inputs staged)
+    placements: dict[str, Placement]
+    index: dict[str, int]
+    n_ops: int
+    arena_bytes: int
+    outputs: tuple[str, ...]
+    inputs: tuple[str, ...]
+    skipped_reshapes: int
+    op_names: tuple[str, ...] = field(default=())
+    op_specs: tuple[str, ...] = field(default=())
+    const_bytes: int = 0
+
+
+def _spec_for(op, graph: Graph, weight_layout: str | None) -> tuple[str, RunnerSpec]:
+    dtypes = [graph.tensor(n).dtype for n in op.inputs]
+    name, spec = select(op.kind, dict(op.attrs), dtypes, weight_layout)
+    spec.check_requires(dict(op.attrs))
+    return name, spec
+
+
+def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
+                           weight_layout: str | None = None, fuse_first: bool = True,
+                           fd: int = 0) -> WholePlanBatch:
+    g = fuse(graph) if fuse_first else graph
+    tensors = g.tensors
+    io = set(g.inputs) | set(g.outputs)
+    consts = {n for n, t in tensors.items() if t.const}
+
+    reshape_src: dict[str, str] = {}
+    for op in g.ops:
+        if op.kind == "reshape":
+            reshape_src[op.outputs[0]] = op.inputs[0]
+    aliased_io = sorted(n for n in reshape_src if n in io)
+    if aliased_io:
+        raise WholePlanError(f"graph inputs/outputs produced by reshape: {aliased_io}")
+
+    def owner(name: str) -> str:
+        seen = {name}
+        while name in reshape_src:
+            name = reshape_src[name]
+            if name in seen:
+                raise WholePlanError(f"reshape cycle at {name!r}")
+            seen.add(name)
+        return name
+
+    layout_of: dict[str, str] = {}
+    dtype_of: dict[str, str] = {}
+
+    def claim(table, name, value, where):
+        prev = table.setdefault(name, value)
+        if prev != value:
+            raise WholePlanError(f"{name!r} is used as {prev!r} and {value!r} ({where})")
+
+    op_specs: dict[int, tuple[str, RunnerSpec]] = {}
+    for op in g.ops:
+        if op.kind == "reshape":
+            continue
+        name, spec = _spec_for(op, g, weight_layout)
+        op_specs[op.id] = (name, spec)
+        lays = spec.buf_layouts()
+        for i, n in enumerate(op.inputs):
+            claim(layout_of, n, lays[i], f"op {op.id} src{i}")
+            claim(dtype_of, n, spec.inputs[i], f"op {op.id} src{i}")
+        for n in op.outputs:
+            claim(layout_of, n, lays[-1], f"op {op.id} dst")
+            claim(dtype_of, n, spec.out_dtype, f"op {op.id} dst")
+
+    def wdtype(n):
+        return dtype_of.get(n, tensors[n].dtype)
+
+    def wbytes(n):
+        return ir_nbytes(tensors[n].shape, wdtype(n))
+
+    placements: dict[str, Placement] = {}
+
+    def place(n, off, region):
+        placements[n] = Placement(n, off, wbytes(n), wdtype(n), layout_of.get(n, "row_major"),
+                                  wire.pad_ne(tensors[n].shape), region, tensors[n].shape)
+
+    cursor = 0
+    for n in sorted(consts):
+        place(n, cursor, "const")
+        cursor = align_up(cursor + wbytes(n))
+    const_end = cursor
+    acts = [n for n in tensors if n not in consts and n not in io and n not in reshape_src]
+    retyped = [n for n in acts if wdtype(n) != tensors[n].dtype]
+    if retyped:
+        raise WholePlanError(f"activations staged in another dtype than declared: {retyped[:6]}")
+    for n in sorted(acts):
+        place(n, cursor, "act")
+        cursor = align_up(cursor + wbytes(n))
+    for n in sorted(io):
+        place(n, cursor, "io")
+        cursor = align_up(cursor + wbytes(n))
+    for n in reshape_src:
+        base = placements.get(owner(n))
+        if base is None:
+            raise WholePlanError(f"reshape {n!r} resolves to unplaced {owner(n)!r}")
+        if wbytes(n) != base.nbytes:
+            raise WholePlanError(f"reshape {n!r} changes the byte count")
+        placements[n] = Placement(n, base.offset, base.nbytes, wdtype(n),
+                                  layout_of.get(n, "row_major"), wire.pad_ne(tensors[n].shape),
+                                  "reshape-alias", tensors[n].shape)
+    arena = align_up(max(cursor, ALIGN))
+
+    payload = bytearray(arena)
+    for n in sorted(consts) + sorted(g.inputs):
+        if n not in feeds:
+            raise WholePlanError(f"no feed for {n!r}")
+        p = placements[n]
+        value = feeds[n]
+        if p.dtype in WIRE_RAW:
+            if isinstance(value, (bytes, bytearray)):
+                data = bytes(value)
+            elif p.layout == "q4_0_kgroup":
+                data = pack_q4_0_kgrouped(np.asarray(value))
+            else:
+                data = pack_q4_0_nblocked(np.asarray(value))
+        else:
+            data = np.ascontiguousarray(np.asarray(value), dtype=_NP[p.dtype]).tobytes()
+        if len(data) != p.nbytes:
+            raise WholePlanError(f"feed {n!r} staged {len(data)} bytes, expected {p.nbytes}")
+        payload[p.offset:p.offset + p.nbytes] = data
+
+    order = sorted(placements)
+    index = {n: i for i, n in enumerate(order)}
+    wtensors = [wire.TensorDesc(0, placements[n].offset, placements[n].nbytes,
+                                placements[n].dtype, placements[n].layout, placements[n].ne)
+                for n in order]
+    ops, names, specs = [], [], []
+    skipped = 0
+    for op in g.ops:
+        if op.kind == "reshape":
+            skipped += 1
+            continue
+        spec_name, spec = op_specs[op.id]
+        shapes = [tensors[n].shape for n in op.inputs]
+        ops.append(wire.OpDesc(kind=KIND_ID[spec_name], params=spec.params(shapes, op.attrs),
+                               src=tuple(index[n] for n in op.inputs),
+                               dst=tuple(index[n] for n in op.outputs)))
+        names.append(f"{op.id}:{spec_name}")
+        specs.append(spec_name)
+    blob = wire.pack_batch([wire.BufDesc(fd=fd, size=arena)], wtensors, ops)
+    return WholePlanBatch(blob=blob, payload=payload, placements=placements, index=index,
+                          n_ops=len(ops), arena_bytes=arena, outputs=tuple(g.outputs),
+                          inputs=tuple(g.inputs), skipped_reshapes=skipped,
+                          op_names=tuple(names), op_specs=tuple(specs), const_bytes=const_end)
+
+
+def decode(batch: WholePlanBatch, name: str, raw: bytes) -> np.ndarray:
+    """Interpret `raw` (the arena bytes of tensor `name`) as float32."""
+    p = batch.placements[name]
+    arr = np.frombuffer(raw, dtype=_NP[p.dtype], count=int(np.prod(p.shape)))
+    return arr.reshape(p.shape).astype(np.float32)

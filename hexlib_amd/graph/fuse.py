@@ -1,0 +1,79 @@
+"""Fusion pass: matmul -> add(const 1-D bias) [-> gelu] becomes matmul_epilogue.
+
+Same rewrite rule as the reference (`hexlib/graph/fuse.py:16-92`): the matmul
+output and the add output must each have exactly one consumer and not be a
+graph output; the bias must be a const rank-1 tensor on either side of the
+add; an activation is folded only if it is gelu_tanh or gelu_erf. Residual
+adds (activation + activation) never fuse.
+"""
+from __future__ import annotations
+
+from hexlib_amd.graph.ir import Graph, Op
+
+FUSABLE_ACTS = ("gelu_tanh", "gelu_erf")
+
+
+class FuseError(ValueError):
+    pass
+
+
+def fuse(graph: Graph) -> Graph:
+    problems = graph.problems()
+    if problems:
+        raise FuseError("graph is structurally invalid:\n" + "\n".join(problems))
+
+    readers: dict[str, list[Op]] = {}
+    for op in graph.ops:
+        for name in op.inputs:
+            readers.setdefault(name, []).append(op)
+    outputs = set(graph.outputs)
+
+    def only_reader(name: str, skip: set[int]) -> Op | None:
+        if name in outputs:
+            return None
+        found = [op for op in readers.get(name, ()) if op.id not in skip]
+        if len(readers.get(name, ())) != 1 or len(found) != 1:
+            return None
+        return found[0]
+
+    absorbed: set[int] = set()
+    replaced: dict[int, Op] = {}
+    dropped: set[str] = set()
+
+    for op in graph.ops:
+        if op.kind != "matmul" or op.id in absorbed:
+            continue
+        mm_out = op.outputs[0]
+        add = only_reader(mm_out, absorbed)
+        if add is None or add.kind != "add":
+            continue
+        if len(add.inputs) != 2:
+            raise FuseError(f"op {add.id} (add) has {len(add.inputs)} inputs")
+        other = [n for n in add.inputs if n != mm_out]
+        if len(other) != 1:
+            continue
+        bias = graph.tensors.get(other[0])
+        if bias is None or not bias.const or len(bias.shape) != 1:
+            continue
+        act, tail = "none", add
+        nxt = only_reader(add.outputs[0], absorbed | {add.id})
+        if nxt is not None and nxt.kind in FUSABLE_ACTS:
+            act, tail = nxt.kind, nxt
+        replaced[op.id] = Op(
+            id=op.id,
+            kind="matmul_epilogue",
+            inputs=(op.inputs[0], op.inputs[1], bias.name),
+            outputs=tail.outputs,
+            attrs={"act": act},
+        )
+        absorbed.add(add.id)
+        dropped.add(mm_out)
+        if tail is not add:
+            absorbed.add(tail.id)
+            dropped.add(add.outputs[0])
+
+    if not replaced:
+        return graph
+    ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
+    tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
+    return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)

@@ -1,0 +1,259 @@
+/* include/hexlib_gpu.h -- the C ABI of libhexlib_gpu.so (MI355X / gfx950).
+ *
+ * Three layers, each a drop-in for one reference interface:
+ *
+ *  1. Per-kernel functions with the exact names, argument orders and scalar
+ *     types of the reference's kernel_api.h headers. Pointers are DEVICE
+ *     pointers; work is enqueued on the library's current HIP stream
+ *     (hexlib_gpu_set_stream) and the call returns without waiting. Invalid
+ *     dimensions make the call a silent no-op, as in the reference.
+ *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
+ *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
+ *     KIND_ID (1-12) plus appended ids 13-16. Generated from the host's
+ *     RunnerSpec table (hexlib_amd/exec/genentry.py).
+ *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
+ *     stop/close/hwinfo) that validates a batch blob on the host, resolves
+ *     tensors through registered device buffers (no address ever crosses the
+ *     wire), and runs every op -- optionally captured once into a hipGraph
+ *     and replayed.
+ *
+ * hexlib_hf is IEEE binary16 storage, bit-compatible with the reference's
+ * `typedef __fp16 hexlib_hf`; it is only ever passed by pointer.
+ */
+#ifndef HEXLIB_GPU_H
+#define HEXLIB_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t hexlib_hf;
+
+/* ---- wire constants: hexlib/runtime/skel/hexlib_dsp.h:21-29 ---- */
+#define HEXLIB_BATCH_MAGIC   0x424C5848u
+#define HEXLIB_BATCH_VERSION 1u
+#define HEXLIB_MAX_BUFS      8
+#define HEXLIB_MAX_SRC       6
+#define HEXLIB_MAX_DST       4
+#define HEXLIB_MAX_PARAMS    16
+/* The DSP bounds a blob at 512 tensors because its working copies are static
+ * (skel_dispatch.c:137-147); the GPU session keeps them on the heap and accepts
+ * up to 4096, so batched encoder plans (about 600 tensors at batch 32) fit.
+ * The wire layout does not depend on this bound. */
+#define HEXLIB_MAX_TENSORS   4096
+#define HEXLIB_MAX_MMAPS     32
+#define HEXLIB_NO_TENSOR     0xFFFFu
+
+/* Status codes: hexlib/runtime/skel/hexlib_dsp.h:34-54. OK is 1. */
+enum hexlib_dsp_status {
+    HEXLIB_DSP_OK = 1,
+    HEXLIB_DSP_ERR_INTERNAL = 2,
+    HEXLIB_DSP_ERR_BAD_MAGIC = 3,
+    HEXLIB_DSP_ERR_BAD_VERSION = 4,
+    HEXLIB_DSP_ERR_TRUNCATED = 5,
+    HEXLIB_DSP_ERR_INVAL_PARAMS = 6,
+    HEXLIB_DSP_ERR_UNMAPPED = 7,
+    HEXLIB_DSP_ERR_NO_MMAP_SLOT = 8,
+    HEXLIB_DSP_ERR_MMAP_FAILED = 9,
+    HEXLIB_DSP_ERR_NO_KERNEL = 10,
+    HEXLIB_DSP_ERR_VTCM_TOO_SMALL = 11,
+    HEXLIB_DSP_ERR_VTCM_RECLAIMED = 12,
+    HEXLIB_DSP_ERR_REQUIRES = 13,
+    HEXLIB_DSP_ERR_NOT_STARTED = 14,
+    HEXLIB_DSP_ERR_CACHE = 15
+};
+
+/* Layout ids: hexlib_dsp.h:168-170, plus 3 = q4_0 grouped along K of W^T. */
+#define HEXLIB_LAYOUT_ROW_MAJOR     0u
+#define HEXLIB_LAYOUT_TILED_32X32   1u
+#define HEXLIB_LAYOUT_Q4_0_REPACKED 2u
+#define HEXLIB_LAYOUT_Q4_0_KGROUP   3u
+
+/* Dtype ids: hexlib/runtime/wire.py:61. */
+#define HEXLIB_DTYPE_FP32  0u
+#define HEXLIB_DTYPE_FP16  1u
+#define HEXLIB_DTYPE_Q4_0  2u
+#define HEXLIB_DTYPE_INT32 3u
+#define HEXLIB_DTYPE_Q8_0  4u
+
+/* Wire structs: byte-identical to hexlib_dsp.h:144-197. `base` and `data`
+ * are resolver scratch; the host writes 0 and the library never reads them. */
+struct hexlib_batch_hdr {
+    uint32_t magic, version, total_size, n_bufs, n_tensors, n_ops;
+    uint32_t off_bufs, off_tensors, off_ops, flags;
+};
+struct hexlib_buf_desc {
+    uint64_t base;
+    uint64_t size;
+    uint32_t fd;
+    uint32_t flags;
+};
+struct hexlib_tensor {
+    uint32_t bi, offset, nbytes, dtype, layout;
+    uint32_t ne[4];
+    uint32_t data, pad;
+};
+struct hexlib_op_desc {
+    uint32_t kind;
+    uint32_t flags;
+    int32_t  params[HEXLIB_MAX_PARAMS];
+    uint16_t src[HEXLIB_MAX_SRC];
+    uint16_t dst[HEXLIB_MAX_DST];
+};
+struct hexlib_batch_rsp_hdr {
+    uint32_t magic, version, status, n_ops;
+    uint64_t cycles_total;   /* GPU nanoseconds (TIMED invokes), else 0 */
+    uint32_t arch;           /* 950 */
+    uint32_t pad;
+};
+struct hexlib_op_result {
+    uint32_t kind;
+    uint32_t status;
+    uint64_t cycles;         /* GPU nanoseconds (TIMED invokes), else 0 */
+};
+
+/* Kernel entry ABI: hexlib_dsp.h:186-198. `vtcm`/`vtcm_size` are always
+ * NULL/0 here: each kernel sizes its own LDS tiles statically. */
+typedef struct {
+    void       *buf[HEXLIB_MAX_BUFS];
+    uint32_t    ne[HEXLIB_MAX_BUFS][4];
+    uint32_t    dtype[HEXLIB_MAX_BUFS];
+    uint32_t    layout[HEXLIB_MAX_BUFS];
+    uint32_t    n_buf;
+    uint8_t    *vtcm;
+    size_t      vtcm_size;
+    const void *params;
+    uint32_t    n_threads;
+} hexlib_args;
+
+typedef int (*hexlib_kernel_fn)(const hexlib_args *);
+
+struct hexlib_kernel_entry {
+    uint32_t         kind;
+    const char      *name;
+    hexlib_kernel_fn fn;
+};
+
+extern const struct hexlib_kernel_entry hexlib_kernel_table[];
+extern const uint32_t hexlib_kernel_table_len;
+
+/* ---- 1. per-kernel API (device pointers) ---- */
+
+/* kernels/add_fp16/kernel_api.h:35 -- y = fp16(float(a) + float(b)). */
+void add_fp16(const hexlib_hf *a, const hexlib_hf *b, hexlib_hf *y, int n);
+/* kernels/scale_fp16/kernel_api.h:37 -- y = fp16(float(x) * factor). */
+void scale_fp16(const hexlib_hf *x, hexlib_hf *y, int n, float factor);
+/* kernels/cast_f32_f16/kernel_api.h:33 -- y = fp16(x), round to nearest even. */
+void cast_f32_f16(const float *x, hexlib_hf *y, int n);
+/* kernels/softmax_fp16/kernel_api.h:69 -- row softmax over C, fp32 inside. */
+void softmax_fp16(const hexlib_hf *x, hexlib_hf *y, int R, int C);
+/* kernels/layernorm_fp16/kernel_api.h:38-39 -- biased variance, fp32 affine. */
+void layernorm_fp16(const hexlib_hf *x, const float *w, const float *b,
+                    hexlib_hf *y, int R, int C, float eps);
+/* kernels/rmsnorm_fp16/kernel_api.h:26-27 -- x * rsqrt(mean(x^2)+eps) * w. */
+void rmsnorm_fp16(const hexlib_hf *x, const hexlib_hf *w,
+                  hexlib_hf *y, int R, int C, float eps);
+/* kernels/rope_2d_fp16/kernel_api.h:120-121 -- split-half rotation, tables [T,D]. */
+void rope_2d_fp16(const hexlib_hf *x, const float *costab, const float *sintab,
+                  hexlib_hf *y, int T, int H, int D);
+/* kernels/transpose_th_fp16/kernel_api.h:38 -- [T,H,D] -> [H,T,D]. */
+void transpose_th_fp16(const hexlib_hf *x, hexlib_hf *y, int T, int H, int D);
+/* kernels/transpose_hd_fp16/kernel_api.h:67 -- [B,T,D] -> [B,D,T]. */
+void transpose_hd_fp16(const hexlib_hf *x, hexlib_hf *y, int B, int T, int D);
+/* kernels/patchify_fp32/kernel_api.h:116-118 -- merge-block token order. */
+void patchify_fp32(const float *img, float *out, int C, int T, int H, int W,
+                   int patch, int merge, int grid_h, int grid_w);
+/* kernels/matmul_fp16/kernel_api.h:77-78 -- batched A[b]@B[b], fp32 sum. */
+void matmul_fp16(const hexlib_hf *A, const hexlib_hf *B, hexlib_hf *C,
+                 int Bn, int M, int K, int N);
+/* kernels/matmul_epilogue_fp16/kernel_api.h:188-190 -- act(a @ deq(w) + bias),
+ * w = q4_0 [K, N] blocked along N; act 0 none / 1 gelu_tanh / 2 gelu_erf. */
+void matmul_epilogue_fp16(const hexlib_hf *a, const unsigned char *w,
+                          const float *bias, hexlib_hf *out,
+                          int M, int K, int N, int act);
+
+/* Extensions (no kernel_api.h counterpart; each serves one appended KIND_ID
+ * or the batch axis of the encoder plan). */
+/* [B,T,H,D] -> [B,H,T,D] (KIND 16); B = 1 is transpose_th_fp16. */
+void transpose_bth_fp16(const hexlib_hf *x, hexlib_hf *y, int B, int T, int H, int D);
+/* patchify over `batch` images stacked as [batch*C, T, H, W] (KIND 6 with
+ * params[4] = batch; batch <= 1 is patchify_fp32). */
+void patchify_fp32_batched(const float *img, float *out, int BC, int T, int H, int W,
+                           int patch, int merge, int grid_h, int grid_w, int batch);
+/* act(a @ w + bias), w fp16 [K, N] row-major (KIND 14). bias may be NULL. */
+void matmul_epilogue_f16w_fp16(const hexlib_hf *a, const hexlib_hf *w,
+                               const float *bias, hexlib_hf *out,
+                               int M, int K, int N, int act);
+/* act(a @ deq(w) + bias), w = q4_0 blocks of 32 along K of W^T [N, K] --
+ * llama.cpp's native Linear layout (KIND 15). bias may be NULL. */
+void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
+                              const float *bias, hexlib_hf *out,
+                              int M, int K, int N, int act);
+
+/* ---- 2. entry adapters (generated) ---- */
+int add_fp16_entry(const hexlib_args *a);
+int scale_fp16_entry(const hexlib_args *a);
+int cast_f32_f16_entry(const hexlib_args *a);
+int softmax_fp16_entry(const hexlib_args *a);
+int layernorm_fp16_entry(const hexlib_args *a);
+int rmsnorm_fp16_entry(const hexlib_args *a);
+int rope_2d_fp16_entry(const hexlib_args *a);
+int transpose_th_fp16_entry(const hexlib_args *a);
+int transpose_hd_fp16_entry(const hexlib_args *a);
+int transpose_bth_fp16_entry(const hexlib_args *a);
+int patchify_fp32_batched_entry(const hexlib_args *a);
+int matmul_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_f16w_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_q4k_fp16_entry(const hexlib_args *a);
+
+/* ---- library control ---- */
+/* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the
+ * default stream). Process-wide. */
+void  hexlib_gpu_set_stream(void *stream);
+void *hexlib_gpu_get_stream(void);
+/* The first HIP error any launch hit since the last call, then cleared
+ * (0 = none). The per-kernel API is void, like the reference's; this is how
+ * a caller learns that a launch failed. */
+int   hexlib_gpu_take_error(void);
+const char *hexlib_gpu_error_string(int hip_error);
+const char *hexlib_gpu_status_name(int status);
+/* sizeof of each wire struct, in declaration order above (batch_hdr, buf_desc,
+ * tensor, op_desc, rsp_hdr, op_result, hexlib_args); returns the count. */
+uint32_t hexlib_gpu_struct_sizes(uint32_t *out, uint32_t cap);
+
+/* ---- 3. session: hexlib/runtime/idl/hexlib_iface.idl:28-67 ---- */
+typedef struct hexlib_gpu_ctx hexlib_gpu_ctx;
+
+#define HEXLIB_GPU_INVOKE_DRYRUN 0x1u  /* validate + run entries, launch nothing (no HIP call) */
+#define HEXLIB_GPU_INVOKE_TIMED  0x2u  /* per-op GPU ns into cycles (eager), or total (graph) */
+#define HEXLIB_GPU_INVOKE_GRAPH  0x4u  /* capture the blob into a hipGraph once, replay after */
+#define HEXLIB_GPU_INVOKE_NOSYNC 0x8u  /* return once enqueued; caller synchronises */
+
+/* Host-only allocation of an idle session. */
+int hexlib_gpu_open(hexlib_gpu_ctx **out);
+int hexlib_gpu_close(hexlib_gpu_ctx *ctx);
+/* Binds `device`, creates the session stream (default priority). */
+int hexlib_gpu_start(hexlib_gpu_ctx *ctx, uint32_t sess_id, int device, uint64_t max_vmem);
+int hexlib_gpu_stop(hexlib_gpu_ctx *ctx);
+/* Registers device memory [dev_ptr, dev_ptr+size) under handle `fd`; blobs
+ * name buffers only by fd (the analogue of fastrpc_mmap + HAP_mmap). */
+int hexlib_gpu_mmap(hexlib_gpu_ctx *ctx, uint32_t fd, void *dev_ptr, uint64_t size);
+int hexlib_gpu_munmap(hexlib_gpu_ctx *ctx, uint32_t fd);
+int hexlib_gpu_hwinfo(hexlib_gpu_ctx *ctx, uint32_t *arch, uint32_t *n_cu,
+                      uint32_t *n_threads, uint64_t *lds_per_cu);
+/* hexlib_dispatch_batch (hexlib/runtime/skel/skel_dispatch.c:80-302): the
+ * response is always self-describing; the return value equals its status. */
+int hexlib_gpu_invoke(hexlib_gpu_ctx *ctx, const uint8_t *batch, uint32_t len,
+                      uint8_t *rsp, uint32_t rsp_cap, uint32_t *rsp_len, uint32_t flags);
+/* The session's stream (a hipStream_t). */
+void *hexlib_gpu_session_stream(hexlib_gpu_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HEXLIB_GPU_H */

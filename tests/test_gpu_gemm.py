@@ -1,0 +1,127 @@
+"""GEMM parity on the GPU through the C ABI: matmul_fp16 (batched attention
+shapes and the harness shape), matmul_epilogue_fp16 (q4_0 blocked along N, the
+reference ABI), matmul_epilogue_f16w_fp16 (BASELINE cfg 3 sweep) and
+matmul_epilogue_q4k_fp16 (cfg 5 shapes), each against the oracle with the
+reference harness tolerance (rel 1e-2; abs 1e-3 for matmul, 3e-4 for the
+epilogue, `kernels/matmul_fp16/harness.c:145`,
+`kernels/matmul_epilogue_fp16/harness.c:259-260`)."""
+import numpy as np
+import pytest
+
+from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
+from oracle import kernels as K
+from tests.gpu_util import Dev, h16, report
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev(torch_gpu):
+    return Dev(torch_gpu)
+
+
+def rng(s):
+    return np.random.default_rng(s)
+
+
+@pytest.mark.parametrize("dims", [(12, 256, 64, 256), (12, 256, 256, 64), (3, 40, 128, 200),
+                                  (2, 17, 33, 45), (1, 256, 768, 2304), (12, 784, 64, 784),
+                                  (1, 1, 64, 8)])
+def test_matmul(dev, dims):
+    Bn, M, Kd, N = dims
+    A = h16(rng(1).standard_normal((Bn, M, Kd)))
+    B = h16(rng(2).standard_normal((Bn, Kd, N)) * 0.1)
+    dA, dB, dC = dev.up(A), dev.up(B), dev.empty((Bn, M, N), np.float16)
+    dev.lib.matmul_fp16(dev.ptr(dA), dev.ptr(dB), dev.ptr(dC), Bn, M, Kd, N)
+    dev.check()
+    got, want = dev.down(dC), K.matmul_fp16(A, B)
+    report(f"matmul {dims}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+def test_matmul_misaligned_operands(dev):
+    A = h16(rng(3).standard_normal((2, 24, 40)))
+    B = h16(rng(4).standard_normal((2, 40, 24)))
+    dA, dB, dC = dev.up(A, 2), dev.up(B, 6), dev.empty((2, 24, 24), np.float16, 2)
+    dev.lib.matmul_fp16(dev.ptr(dA), dev.ptr(dB), dev.ptr(dC), 2, 24, 40, 24)
+    dev.check()
+    assert K.close_f16(dev.down(dC), K.matmul_fp16(A, B), 1e-2, 1e-3).all()
+
+
+def _q4_inputs(M, Kd, N, seed):
+    r = rng(seed)
+    a = h16(r.standard_normal((M, Kd)))
+    w = (r.standard_normal((Kd, N)) * r.uniform(0.005, 0.02)).astype(np.float32)
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    return a, w, bias
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(20, 128, 160, 1), (256, 768, 768, 0), (64, 3072, 1024, 2),
+                                        (3, 96, 64, 2), (256, 1536, 768, 0), (1, 896, 4864, 0),
+                                        (16, 4864, 896, 0), (256, 2048, 2048, 0)])
+def test_matmul_epilogue_q4_nblocked(dev, M, Kd, N, act):
+    a, w, bias = _q4_inputs(M, Kd, N, 5)
+    wq = pack_q4_0_nblocked(w)
+    da, dw, db, do = dev.up(a), dev.up(np.frombuffer(wq, np.uint8)), dev.up(bias), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+    dev.check()
+    got, want = dev.down(do), K.matmul_epilogue_fp16(a, wq, bias, Kd, N, act)
+    report(f"q4n {M}x{Kd}x{N} act{act}", got, want)
+    assert K.close_f16(got, want, 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("M,Kd,N", [(1, 896, 4864), (16, 896, 4864), (256, 896, 4864),
+                                    (1, 4864, 896), (16, 4864, 896), (256, 4864, 896),
+                                    (1, 2048, 2048), (16, 2048, 2048), (256, 2048, 2048)])
+def test_matmul_q4k_cfg5(dev, M, Kd, N):
+    """BASELINE cfg 5: nibbles uniform, fp16 scales U(0.005, 0.02), zero point 8,
+    activations N(0,1), no bias, no activation."""
+    r = rng(6)
+    n_blocks = N * Kd // 32
+    blocks = np.empty((n_blocks, 18), np.uint8)
+    blocks[:, :2] = r.uniform(0.005, 0.02, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = r.integers(0, 256, (n_blocks, 16), dtype=np.uint8)
+    wq = blocks.tobytes()
+    a = h16(r.standard_normal((M, Kd)))
+    bias = np.zeros(N, np.float32)
+    da, dw, db, do = dev.up(a), dev.up(blocks), dev.up(bias), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_q4k_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, 0)
+    dev.check()
+    got, want = dev.down(do), K.matmul_q4k(a, wq, bias, Kd, N, 0)
+    report(f"q4k {M}x{Kd}x{N}", got, want)
+    assert K.close_f16(got, want, 0.01, 3e-4).all()
+
+
+def test_q4k_and_nblocked_agree_on_the_same_weight(dev):
+    a, w, bias = _q4_inputs(64, 256, 128, 7)
+    outs = []
+    for fn, wq in (("matmul_epilogue_q4k_fp16", pack_q4_0_kgrouped(w)),
+                   ("matmul_epilogue_fp16", pack_q4_0_nblocked(w))):
+        da, dw, db, do = dev.up(a), dev.up(np.frombuffer(wq, np.uint8)), dev.up(bias), dev.empty((64, 128), np.float16)
+        getattr(dev.lib, fn)(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), 64, 256, 128, 1)
+        dev.check()
+        outs.append(dev.down(do))
+    # Both quantize the same weight along different axes: each must track the
+    # unquantized product closely; they differ from each other only by format error.
+    dense = K.gemm_epilogue(a, w.astype(np.float16).astype(np.float32), bias, 1).astype(np.float64)
+    for o in outs:
+        assert np.corrcoef(o.astype(np.float64).ravel(), dense.ravel())[0, 1] > 0.98
+
+
+@pytest.mark.parametrize("M,Kd,N,act,scale", [(256, 768, 2304, 1, 0.02), (256, 768, 768, 0, 0.02),
+                                              (256, 768, 3072, 1, 0.02), (256, 3072, 768, 0, 0.02),
+                                              (256, 768, 768, 1, 1.0), (64, 3072, 3072, 2, 1.0),
+                                              (8192, 768, 768, 1, 1.0), (17, 40, 24, 2, 1.0)])
+def test_matmul_epilogue_f16w(dev, M, Kd, N, act, scale):
+    """BASELINE cfg 3 (A/B ~ N(0, 0.02), bias + GELU) plus unit-scale cases
+    where the absolute tolerance cannot hide a wrong product."""
+    r = rng(8)
+    a = h16(r.standard_normal((M, Kd)) * scale)
+    w = h16(r.standard_normal((Kd, N)) * (0.02 if scale < 1 else 1.0 / np.sqrt(Kd)))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dw, db, do = dev.up(a), dev.up(w), dev.up(bias), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_f16w_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+    dev.check()
+    got, want = dev.down(do), K.matmul_epilogue_f16w(a, w, bias, act)
+    report(f"f16w {M}x{Kd}x{N} act{act}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()

@@ -1,0 +1,161 @@
+"""Whole-plan parity on the GPU: one blob, one arena, every op through the
+dispatcher and the generated entries, eager and as one captured hipGraph.
+
+Compared with the oracle's storage-rounding executor (`oracle.eager.run_stored`,
+the reference `interpreter.run` numerics) on the same seeded feeds; BASELINE's
+whole-encoder bar is 2e-2 max abs. Graph replays are checked against the eager
+run bit for bit, several times over with eager work in between.
+"""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from hexlib_amd import encoder as E
+from hexlib_amd.exec.gpu import GpuBackend, GpuPlan, GpuSession
+from hexlib_amd.exec.wholeplan import build_whole_plan_batch
+from hexlib_amd.graph.fuse import fuse
+from oracle import eager
+from oracle.quant import dequantize_q4_0_fp16
+from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def session(torch_gpu):
+    s = GpuSession()
+    yield s
+    s.close()
+
+
+def _run_plan(session, cfg, feeds, graph_mode, weight_layout=None, repeats=1):
+    g = E.build_vision_encoder(cfg)
+    wb = build_whole_plan_batch(g, feeds, weight_layout=weight_layout)
+    plan = GpuPlan(wb, session)
+    try:
+        outs = []
+        for _ in range(repeats):
+            rsp = plan.run(graph=graph_mode)
+            assert rsp.ok and rsp.n_ops == wb.n_ops
+            outs.append(plan.read(g.outputs[0]))
+        return outs, wb
+    finally:
+        plan.close()
+
+
+def _oracle(cfg, feeds, dense_weights=None):
+    g = fuse(E.build_vision_encoder(cfg))
+    f = dict(feeds)
+    if dense_weights:
+        f.update(dense_weights)
+    return eager.run_stored(g, f)[g.outputs[0]]
+
+
+@pytest.mark.parametrize("cfg", [E.TINY_ENCODER, replace(E.TINY_ENCODER, norm="layernorm")])
+def test_tiny_encoder_eager_and_graph(session, cfg):
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg, seed=0)
+    want = _oracle(cfg, feeds)
+    (eager_out,), _ = _run_plan(session, cfg, feeds, graph_mode=False)
+    graph_outs, _ = _run_plan(session, cfg, feeds, graph_mode=True, repeats=3)
+    err = np.abs(eager_out - want).max()
+    print(f"[tiny {cfg.norm}] max abs vs oracle {err:.3e}", flush=True)
+    assert err <= 2e-2
+    for o in graph_outs:
+        np.testing.assert_array_equal(o, eager_out)
+
+
+def test_golden_config_fp16_on_gpu(session, golden):
+    cfg = replace(E.GOLDEN_TINY, act_dtype="fp16", weight_dtype="fp16")
+    g = E.build_vision_encoder(cfg)
+    feeds = E.feeds_from_params(g, cfg, lambda n: golden["param::" + n])
+    feeds = {k: (v.astype(np.float16).astype(np.float32) if g.tensor(k).dtype == "fp16" else v)
+             for k, v in feeds.items()}
+    feeds["image"] = golden["image"]
+    (out,), _ = _run_plan(session, cfg, feeds, graph_mode=True)
+    want = _oracle(cfg, feeds)
+    up = golden["expected_merged"]
+    print(f"[golden fp16] vs oracle {np.abs(out - want).max():.3e} vs upstream {np.abs(out - up).max():.3e}",
+          flush=True)
+    assert np.abs(out - want).max() <= 2e-2
+    assert np.abs(out - up).max() <= 2e-2
+
+
+def test_qwen_encoder_256_fp16(session):
+    cfg = E.QWEN35_VISION_FP16
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg, seed=0)
+    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True)
+    assert wb.n_ops == 259
+    want = _oracle(cfg, feeds)
+    err = np.abs(out - want).max()
+    print(f"[qwen 256 fp16] max abs {err:.3e} (|out| max {np.abs(want).max():.3f})", flush=True)
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize("layout", [None, "q4_0_kgroup"])
+def test_qwen_encoder_reference_q4_config(session, layout):
+    """The reference's own shipped config: T=2, q4_0 weights. The oracle gets
+    the dequantized, fp16-rounded weights the kernel multiplies with."""
+    cfg = replace(E.QWEN35_VISION_Q4, depth=2)
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg, seed=1)
+    dense = {}
+    for t in g.tensors.values():
+        if t.dtype == "q4_0":
+            w = feeds[t.name]
+            if layout == "q4_0_kgroup":
+                dq = dequantize_q4_0_fp16(pack_q4_0_kgrouped(w), w.shape[::-1]).T
+            else:
+                dq = dequantize_q4_0_fp16(pack_q4_0_nblocked(w), w.shape)
+            dense[t.name] = np.ascontiguousarray(dq)
+    (out,), _ = _run_plan(session, cfg, feeds, graph_mode=True, weight_layout=layout)
+    want = _oracle(cfg, feeds, dense)
+    err = np.abs(out - want).max()
+    print(f"[qwen q4 {layout}] max abs {err:.3e}", flush=True)
+    assert err <= 2e-2
+
+
+def test_batched_encoder_matches_per_image(session):
+    cfg1 = E.TINY_ENCODER
+    cfgb = replace(cfg1, batch=3)
+    gb = E.build_vision_encoder(cfgb)
+    feeds_b = E.synthetic_feeds(gb, cfgb, seed=2)
+    (out_b,), _ = _run_plan(session, cfgb, feeds_b, graph_mode=True)
+    g1 = E.build_vision_encoder(cfg1)
+    per = out_b.shape[0] // 3
+    for i in range(3):
+        f1 = {}
+        for t in g1.tensors.values():
+            if t.name == "image":
+                f1["image"] = feeds_b["image"][i * 3:(i + 1) * 3]
+            elif t.name in ("pos_embed", "rope_cos", "rope_sin"):
+                n = cfg1.num_tokens
+                f1[t.name] = feeds_b[t.name][i * n:(i + 1) * n]
+            elif t.const:
+                f1[t.name] = feeds_b[t.name]
+        want = _oracle(cfg1, f1)
+        assert np.abs(out_b[i * per:(i + 1) * per] - want).max() <= 2e-2
+
+
+def test_per_op_backend_through_the_wire(session):
+    be = GpuBackend(session)
+    r = np.random.default_rng(3)
+    x = r.standard_normal((12, 256, 64)).astype(np.float16)
+    y, rsp = be.run("transpose", [x], {"perm": (0, 2, 1)}, (12, 64, 256))
+    np.testing.assert_array_equal(y, np.transpose(x, (0, 2, 1)))
+    assert rsp.results[0].cycles > 0                      # timed: GPU ns
+    s = (r.standard_normal((12, 256, 256)) * 0.125).astype(np.float16)
+    y, _ = be.run("softmax", [s], {"axis": -1}, s.shape)
+    xs = s.astype(np.float64)
+    want = np.exp(xs - xs.max(-1, keepdims=True))
+    want /= want.sum(-1, keepdims=True)
+    assert np.abs(y.astype(np.float64) - want).max() <= 2e-3
+    a = r.standard_normal((64, 128)).astype(np.float16)
+    w = (r.standard_normal((128, 96)) * 0.05).astype(np.float32)
+    b = np.zeros(96, np.float32)
+    y, _ = be.run("matmul_epilogue", [a, w, b], {"act": "gelu_tanh"}, (64, 96))
+    from oracle import kernels as K
+    want = K.matmul_epilogue_fp16(a, pack_q4_0_nblocked(w), b, 128, 96, 1)
+    assert K.close_f16(y, want, 0.01, 3e-4).all()

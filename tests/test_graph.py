@@ -1,0 +1,116 @@
+"""Graph, fusion, dispatch-table and whole-plan invariants (CPU).
+
+Restates the reference's coverage tests (`hexlib/tests/test_encoder_dispatch_coverage.py`,
+`test_runtime_genentry.py`, `test_pass_fuse.py`, `test_wholeplan.py:44-160`).
+"""
+import collections
+
+import numpy as np
+import pytest
+
+from hexlib_amd import encoder as E
+from hexlib_amd.exec import wholeplan as WP
+from hexlib_amd.exec.runner import KIND_ID, SPECS, SelectError, select
+from hexlib_amd.graph.fuse import fuse
+from hexlib_amd.graph.ir import Graph, Op, Tensor
+
+
+@pytest.fixture(scope="module")
+def qwen_fused():
+    return fuse(E.build_vision_encoder(E.QWEN35_VISION_Q4))
+
+
+def test_plan_is_the_reference_size(qwen_fused):
+    kinds = collections.Counter(op.kind for op in qwen_fused.ops)
+    assert len(qwen_fused.ops) == 308
+    assert kinds["reshape"] == 49
+    assert kinds["matmul"] == 24
+    assert kinds["matmul_epilogue"] == 75
+
+
+def test_every_non_reshape_op_selects_a_kernel(qwen_fused):
+    for op in qwen_fused.ops:
+        if op.kind == "reshape":
+            continue
+        dtypes = [qwen_fused.tensor(n).dtype for n in op.inputs]
+        select(op.kind, dict(op.attrs), dtypes)
+
+
+def test_shipped_kind_ids_never_move():
+    assert {k: KIND_ID[k] for k in list(KIND_ID)[:12]} == {
+        "add": 1, "cast": 2, "layernorm": 3, "matmul": 4, "matmul_epilogue": 5,
+        "patchify": 6, "reshape": 7, "rope_2d": 8, "scale": 9, "softmax": 10,
+        "transpose": 11, "transpose_hd": 12}
+    assert len(set(KIND_ID.values())) == len(KIND_ID)
+
+
+def test_every_spec_has_a_kind_id():
+    assert set(SPECS) <= set(KIND_ID)
+
+
+def test_variant_selection():
+    assert select("transpose", {"perm": (1, 0, 2)})[0] == "transpose"
+    assert select("transpose", {"perm": (0, 2, 1)})[0] == "transpose_hd"
+    assert select("transpose", {"perm": (0, 2, 1, 3)})[0] == "transpose_bth"
+    with pytest.raises(SelectError):
+        select("transpose", {"perm": (2, 1, 0)})
+    assert select("matmul_epilogue", {"act": "none"})[0] == "matmul_epilogue"
+    assert select("matmul_epilogue", {"act": "none"}, ["fp16", "fp16", "fp32"])[0] == "matmul_epilogue_f16w"
+    assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q4_0", "fp32"])[0] == "matmul_epilogue"
+    assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q4_0", "fp32"],
+                  "q4_0_kgroup")[0] == "matmul_epilogue_q4k"
+    with pytest.raises(SelectError):
+        select("softmax", {"axis": 0})
+
+
+def test_fuse_folds_bias_and_gelu_but_not_residuals():
+    t = {n: Tensor(n, "fp32", s, c) for n, s, c in [
+        ("x", (4, 8), False), ("w", (8, 8), True), ("b", (8,), True), ("mm", (4, 8), False),
+        ("y", (4, 8), False), ("g", (4, 8), False), ("r", (4, 8), False)]}
+    ops = (Op(0, "matmul", ("x", "w"), ("mm",)), Op(1, "add", ("b", "mm"), ("y",)),
+           Op(2, "gelu_erf", ("y",), ("g",)), Op(3, "add", ("x", "g"), ("r",)))
+    f = fuse(Graph(t, ops, ("x",), ("r",)))
+    assert [op.kind for op in f.ops] == ["matmul_epilogue", "add"]
+    assert f.ops[0].attrs["act"] == "gelu_erf" and f.ops[0].inputs == ("x", "w", "b")
+
+
+def test_batched_graph_shapes():
+    from dataclasses import replace
+    cfg = replace(E.TINY_ENCODER, batch=3)
+    g = fuse(E.build_vision_encoder(cfg))
+    assert g.tensor("image").shape == (9, 1, 64, 64)
+    assert g.tensor(g.outputs[0]).shape == (3 * 16 // 4, 64)
+    kinds = collections.Counter(op.kind for op in g.ops)
+    assert kinds["transpose"] == cfg.depth * 5
+
+
+@pytest.mark.parametrize("cfg", [E.TINY_ENCODER, E.QWEN35_VISION_FP16])
+def test_whole_plan_arena_invariants(cfg):
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg)
+    wb = WP.build_whole_plan_batch(g, feeds)
+    own = [p for p in wb.placements.values() if p.region != "reshape-alias"]
+    spans = sorted((p.offset, p.offset + p.nbytes, p.name) for p in own)
+    for (a0, a1, an), (b0, b1, bn) in zip(spans, spans[1:]):
+        assert a1 <= b0, f"{an} overlaps {bn}"
+    assert all(p.offset % WP.ALIGN == 0 for p in own)
+    assert spans[-1][1] <= wb.arena_bytes
+    f = fuse(g)
+    for op in f.ops:
+        if op.kind == "reshape":
+            assert wb.placements[op.outputs[0]].offset == wb.placements[op.inputs[0]].offset
+    assert wb.placements["pos_embed"].dtype == "fp16"
+    assert wb.n_ops + wb.skipped_reshapes == len(f.ops)
+
+
+def test_whole_plan_q4_layouts():
+    from dataclasses import replace
+    cfg = replace(E.TINY_ENCODER, weight_dtype="q4_0", norm="layernorm")
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg)
+    a = WP.build_whole_plan_batch(g, feeds)
+    b = WP.build_whole_plan_batch(g, feeds, weight_layout="q4_0_kgroup")
+    assert set(a.op_specs) >= {"matmul_epilogue"} and "matmul_epilogue_q4k" not in a.op_specs
+    assert "matmul_epilogue_q4k" in b.op_specs
+    assert b.placements["blk0.wq"].layout == "q4_0_kgroup"
+    assert a.placements["blk0.wq"].nbytes == 64 * 64 // 32 * 18

@@ -1,0 +1,243 @@
+"""The C-ABI library on the CPU: it loads, exports every declared symbol, its
+wire structs match the Python serializer byte for byte, the generated entries
+are current, and every refusal of the dispatcher fires before any GPU call.
+
+No compute runs here: DRYRUN invokes validate the blob, resolve tensors and
+run the generated entries' checks, and the API functions return before
+launching (the library makes no HIP call on that path). The refusals restate
+the reference's host-forced failures (`hexlib/exec/dsp.py:565-609`,
+`hexlib/tests/test_dsp_sim.py:43-706`): bad magic, bad version, truncation,
+an unmapped buffer, an unknown kind, a dtype or layout mismatch.
+"""
+import ctypes
+import struct
+
+import numpy as np
+import pytest
+
+from hexlib_amd import lib as L
+from hexlib_amd.exec import genentry, wire
+from hexlib_amd.exec.runner import KIND_ID, SPECS
+
+OK = wire.STATUS["OK"]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return L.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = L.header_functions() + L.header_objects()
+    assert len(names) > 40
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/hexlib_gpu.h but not exported"
+
+
+def test_struct_sizes_match_the_wire(lib):
+    arr = (ctypes.c_uint32 * 8)()
+    n = lib.hexlib_gpu_struct_sizes(arr, 8)
+    assert list(arr)[:6] == [wire.HDR_SIZE, wire.BUF_SIZE, wire.TENSOR_SIZE, wire.OP_SIZE,
+                             wire.RSP_HDR_SIZE, wire.RESULT_SIZE]
+    assert n == 7
+
+
+def test_status_names_agree(lib):
+    for name, code in wire.STATUS.items():
+        assert lib.hexlib_gpu_status_name(code).decode() == name
+
+
+def test_generated_entries_are_current():
+    assert open(genentry.OUT_PATH).read() == genentry.generate()
+
+
+def test_kernel_table_covers_every_spec(lib):
+    n = ctypes.c_uint32.in_dll(lib, "hexlib_kernel_table_len").value
+    assert n == len(SPECS)
+
+
+# ---- dispatcher refusals, all on the host -------------------------------------
+
+class Session:
+    def __init__(self, lib):
+        self.lib = lib
+        self.h = ctypes.c_void_p()
+        assert lib.hexlib_gpu_open(ctypes.byref(self.h)) == OK
+
+    def mmap(self, fd, size, base=0x10000000):
+        return self.lib.hexlib_gpu_mmap(self.h, fd, ctypes.c_void_p(base), size)
+
+    def invoke(self, blob, flags=L.INVOKE_DRYRUN, cap=4096):
+        rsp = ctypes.create_string_buffer(cap)
+        n = ctypes.c_uint32()
+        rc = self.lib.hexlib_gpu_invoke(self.h, blob, len(blob), rsp, cap, ctypes.byref(n), flags)
+        return rc, wire.unpack_response(rsp.raw[:n.value])
+
+    def close(self):
+        self.lib.hexlib_gpu_close(self.h)
+
+
+@pytest.fixture
+def sess(lib):
+    s = Session(lib)
+    yield s
+    s.close()
+
+
+def scale_blob(fd=3, n=4100, dtype_in="fp16", layout="row_major", kind=None, out_n=None,
+               size=None):
+    nb = n * (4 if dtype_in == "fp32" else 2)
+    out_n = n if out_n is None else out_n
+    off_out = (nb + 255) // 256 * 256
+    size = size or off_out + out_n * 2
+    t = [wire.TensorDesc(0, 0, nb, dtype_in, layout, (n, 1, 1, 1)),
+         wire.TensorDesc(0, off_out, out_n * 2, "fp16", "row_major", (out_n, 1, 1, 1))]
+    op = wire.OpDesc(kind if kind is not None else KIND_ID["scale"],
+                     (wire.float_param(0.125),), (0,), (1,))
+    return wire.pack_batch([wire.BufDesc(fd, size)], t, [op]), size
+
+
+def test_dry_run_accepts_a_well_formed_op(sess):
+    blob, size = scale_blob()
+    assert sess.mmap(3, size) == OK
+    rc, rsp = sess.invoke(blob)
+    assert rc == OK and rsp.ok and rsp.arch == 950
+    assert [r.kind for r in rsp.results] == [KIND_ID["scale"]]
+
+
+def test_invoke_before_start_is_refused(sess):
+    blob, size = scale_blob()
+    sess.mmap(3, size)
+    rc, rsp = sess.invoke(blob, flags=0)
+    assert rc == rsp.status == wire.STATUS["ERR_NOT_STARTED"]
+
+
+def test_bad_magic_and_version(sess):
+    blob, size = scale_blob()
+    sess.mmap(3, size)
+    bad = bytearray(blob)
+    bad[0] ^= 1
+    assert sess.invoke(bytes(bad))[0] == wire.STATUS["ERR_BAD_MAGIC"]
+    bad = bytearray(blob)
+    struct.pack_into("<I", bad, 4, 2)
+    assert sess.invoke(bytes(bad))[0] == wire.STATUS["ERR_BAD_VERSION"]
+
+
+def test_truncated_blob_and_response(sess):
+    blob, size = scale_blob()
+    sess.mmap(3, size)
+    assert sess.invoke(blob[:-4])[0] == wire.STATUS["ERR_TRUNCATED"]
+    assert sess.invoke(blob[:10])[0] == wire.STATUS["ERR_TRUNCATED"]
+    assert sess.invoke(blob, cap=wire.RSP_HDR_SIZE)[0] == wire.STATUS["ERR_TRUNCATED"]
+
+
+def test_huge_op_count_cannot_wrap_the_bounds_check(sess):
+    blob, size = scale_blob()
+    sess.mmap(3, size)
+    bad = bytearray(blob)
+    struct.pack_into("<I", bad, 20, 0xFFFFFFFF)
+    assert sess.invoke(bytes(bad))[0] == wire.STATUS["ERR_TRUNCATED"]
+
+
+def test_an_unmapped_fd_is_refused(sess):
+    blob, size = scale_blob(fd=9)
+    sess.mmap(3, size)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_UNMAPPED"]
+
+
+def test_buffer_larger_than_its_mapping_is_refused(sess):
+    blob, size = scale_blob()
+    sess.mmap(3, size - 256)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_INVAL_PARAMS"]
+
+
+def test_unknown_kind_is_no_kernel(sess):
+    blob, size = scale_blob(kind=99)
+    sess.mmap(3, size)
+    rc, rsp = sess.invoke(blob)
+    assert rc == wire.STATUS["ERR_NO_KERNEL"] and rsp.results[0].kind == 99
+
+
+def test_reshape_kind_has_no_kernel(sess):
+    blob, size = scale_blob(kind=KIND_ID["reshape"])
+    sess.mmap(3, size)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_NO_KERNEL"]
+
+
+def test_dtype_and_layout_mismatch_are_requires(sess):
+    blob, size = scale_blob(dtype_in="fp32", n=2050)
+    sess.mmap(3, size)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_REQUIRES"]
+    blob, size = scale_blob(fd=4, layout="tiled_32x32")
+    sess.mmap(4, size, base=0x30000000)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_REQUIRES"]
+
+
+def test_output_smaller_than_the_kernel_writes_is_refused(sess):
+    blob, size = scale_blob(out_n=100)
+    sess.mmap(3, size)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_INVAL_PARAMS"]
+
+
+def test_extent_larger_than_nbytes_is_refused(sess):
+    n = 4100
+    t = [wire.TensorDesc(0, 0, 100, "fp16", "row_major", (n, 1, 1, 1)),
+         wire.TensorDesc(0, 8448, n * 2, "fp16", "row_major", (n, 1, 1, 1))]
+    op = wire.OpDesc(KIND_ID["scale"], (wire.float_param(0.5),), (0,), (1,))
+    blob = wire.pack_batch([wire.BufDesc(3, 8448 + n * 2)], t, [op])
+    sess.mmap(3, 8448 + n * 2)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_INVAL_PARAMS"]
+
+
+def test_bad_activation_code_is_refused(sess):
+    M, K, N = 4, 64, 32
+    sizes = [M * K * 2, K * N // 32 * 18, N * 4, M * N * 2]
+    offs = np.cumsum([0] + [(s + 255) // 256 * 256 for s in sizes])
+    t = [wire.TensorDesc(0, int(offs[0]), sizes[0], "fp16", "row_major", (M, K, 1, 1)),
+         wire.TensorDesc(0, int(offs[1]), sizes[1], "q4_0", "row_major", (K, N, 1, 1)),
+         wire.TensorDesc(0, int(offs[2]), sizes[2], "fp32", "row_major", (N, 1, 1, 1)),
+         wire.TensorDesc(0, int(offs[3]), sizes[3], "fp16", "row_major", (M, N, 1, 1))]
+    for act, want in ((1, "OK"), (7, "ERR_INVAL_PARAMS")):
+        op = wire.OpDesc(KIND_ID["matmul_epilogue"], (act,), (0, 1, 2), (3,))
+        blob = wire.pack_batch([wire.BufDesc(3, int(offs[4]))], t, [op])
+        sess.mmap(3, int(offs[4]))
+        assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+def test_first_failing_op_stops_the_batch(sess):
+    blob, size = scale_blob()
+    hdr = list(struct.unpack_from(wire._HDR, blob))
+    n_ops = 3
+    ops = blob[hdr[8]:] * 1
+    good = ops
+    bad = bytearray(ops)
+    struct.pack_into("<I", bad, 0, 99)
+    body = blob[:hdr[8]] + good + bytes(bad) + good
+    body = bytearray(body)
+    struct.pack_into("<I", body, 8, len(body))
+    struct.pack_into("<I", body, 20, n_ops)
+    sess.mmap(3, size)
+    rc, rsp = sess.invoke(bytes(body))
+    assert rc == wire.STATUS["ERR_NO_KERNEL"]
+    assert rsp.n_ops == 2 and rsp.results[0].ok and rsp.results[1].status == rc
+
+
+def test_mmap_table_limits(sess):
+    for fd in range(32):
+        assert sess.mmap(100 + fd, 256, 0x20000000 + fd * 4096) == OK
+    assert sess.mmap(500, 256, 0x90000000) == wire.STATUS["ERR_NO_MMAP_SLOT"]
+    assert sess.mmap(100, 256, 0x20000000) == OK                        # idempotent
+    assert sess.mmap(100, 512, 0x20000000) == wire.STATUS["ERR_MMAP_FAILED"]
+    assert sess.lib.hexlib_gpu_munmap(sess.h, 100) == OK
+    assert sess.lib.hexlib_gpu_munmap(sess.h, 100) == wire.STATUS["ERR_UNMAPPED"]
+
+
+def test_whole_encoder_blob_dry_runs(sess):
+    from hexlib_amd import encoder as E
+    from hexlib_amd.exec.wholeplan import build_whole_plan_batch
+    cfg = E.TINY_ENCODER
+    g = E.build_vision_encoder(cfg)
+    wb = build_whole_plan_batch(g, E.synthetic_feeds(g, cfg))
+    sess.mmap(0, wb.arena_bytes)
+    rc, rsp = sess.invoke(wb.blob, cap=wire.RSP_HDR_SIZE + wire.RESULT_SIZE * wb.n_ops)
+    assert rc == OK and rsp.n_ops == wb.n_ops and rsp.ok
