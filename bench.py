@@ -74,7 +74,7 @@ def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
 
 # ---- plan helpers -------------------------------------------------------------------------
 
-def build_plan(cfg, seed=0, weight_layout=None):
+def build_plan(cfg, seed=0, weight_layout="auto"):
     from hexlib_amd import encoder as E
     from hexlib_amd.exec.wholeplan import build_whole_plan_batch
     g = E.build_vision_encoder(cfg)
@@ -285,6 +285,31 @@ def cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
                       f"os.cpu_count()={os.cpu_count()}, numpy {np.__version__}"}
 
 
+def run_variant(session, vcfg, steps: int, label: str) -> dict:
+    from hexlib_amd.exec.gpu import GpuPlan
+    gv, _, wbv = build_plan(vcfg)
+    pv = GpuPlan(wbv, session)
+    try:
+        s = time_replays(pv, steps, 3)
+        out = {"images_per_s": round(steps * vcfg.batch / s, 2),
+               "ms_per_step": round(s / steps * 1e3, 3), "batch": vcfg.batch,
+               "tokens": vcfg.num_tokens, "steps": steps}
+        rows = per_op_in_plan(pv, gv, reps=10)
+        mm = [r for r in rows if r["bound"] == "mfma"]
+        fl = sum(r["count"] * r["avg_ns"] * r["achieved"] * 1e3 for r in mm)
+        t = sum(r["count"] * r["avg_ns"] for r in mm)
+        out["gemm_tflops"] = round(fl / t / 1e3, 2) if t else None
+        out["gemm_frac_of_peak"] = round(fl / t / 1e3 / MFMA_FP16_PEAK_TFLOPS, 4) if t else None
+        out["per_op"] = rows
+        log(f"variant {label}: {out['images_per_s']} images/s, GEMMs {out['gemm_tflops']} TFLOP/s")
+        for r in rows:
+            log(f"  {r['op']:22s} x{r['count']:3d} {r['avg_ns']:9.0f} ns  {r['achieved']:9.2f} {r['unit']:7s} "
+                f"({r['frac'] * 100:5.1f}%)  total {r['total_us']:8.1f} us  {r['shape']}")
+        return out
+    finally:
+        pv.close()
+
+
 # ---- main -------------------------------------------------------------------------------
 
 def main() -> int:
@@ -318,6 +343,9 @@ def main() -> int:
 
     log("per-op timing inside the plan")
     per_op = per_op_in_plan(plan, g)
+    for r in per_op:
+        log(f"  {r['op']:22s} x{r['count']:3d} {r['avg_ns']:9.0f} ns  {r['achieved']:9.2f} {r['unit']:7s} "
+            f"({r['frac'] * 100:5.1f}%)  total {r['total_us']:8.1f} us  {r['shape']}")
     plan_gpu_ns = None
     try:
         from hexlib_amd import lib as L
@@ -353,22 +381,11 @@ def main() -> int:
         for label, vcfg, steps in (("256_b32", replace(cfg, batch=32), max(5, args.steps // 10)),
                                    ("448_b1", E.encoder_at(448), max(10, args.steps // 2))):
             log(f"variant {label}")
-            gv, _, wbv = build_plan(vcfg)
-            pv = GpuPlan(wbv, session)
-            s = time_replays(pv, steps, 3)
-            variants[label] = {"images_per_s": round(steps * vcfg.batch / s, 2),
-                               "ms_per_step": round(s / steps * 1e3, 3), "batch": vcfg.batch,
-                               "tokens": vcfg.num_tokens, "steps": steps}
-            if label == "256_b32":
-                rows = per_op_in_plan(pv, gv, reps=10)
-                mm = [r for r in rows if r["bound"] == "mfma"]
-                fl = sum(r["count"] * r["avg_ns"] * r["achieved"] * 1e3 for r in mm)
-                t = sum(r["count"] * r["avg_ns"] for r in mm)
-                variants[label]["gemm_tflops"] = round(fl / t / 1e3, 2) if t else None
-                variants[label]["gemm_frac_of_peak"] = round(fl / t / 1e3 / MFMA_FP16_PEAK_TFLOPS, 4) if t else None
-                variants[label]["per_op"] = rows
-            pv.close()
-            log(f"variant {label}: {variants[label]['images_per_s']} images/s")
+            try:
+                variants[label] = run_variant(session, vcfg, steps, label)
+            except Exception as e:  # noqa: BLE001 -- a variant failure must not lose the headline line
+                log(f"variant {label} failed: {type(e).__name__}: {e}")
+                variants[label] = {"error": f"{type(e).__name__}: {e}"}
 
     suite_rows = [] if args.no_suite else suite(session)
 

@@ -1,40 +1,51 @@
-// fp16 GEMMs on CDNA4 MFMA: matmul_fp16 (batched), matmul_epilogue_f16w_fp16,
-// matmul_epilogue_fp16 (q4_0 blocked along N -- the reference kernel ABI) and
+// fp16 GEMMs on CDNA4 MFMA: matmul_fp16 (batched), matmul_epilogue_f16w_fp16
+// (W [K,N]), matmul_epilogue_f16wt_fp16 (W^T [N,K]), matmul_epilogue_fp16
+// (q4_0 blocked along N -- the reference kernel ABI) and
 // matmul_epilogue_q4k_fp16 (q4_0 grouped along K of W^T).
 //
 // Numerics (kernels/matmul_fp16/kernel_api.h:18-29, kernels/matmul_epilogue_fp16/
 // kernel_api.h:16-27, baseline.c:34-97): fp16 x fp16 products accumulated in
 // fp32 by v_mfma_f32_32x32x16_f16; a q4_0 weight is dequantized to
-// fp16(d * (q - 8)) before it is multiplied (the reference kernel's own
-// rounding); then bias (fp32) is added, the activation applied in fp32, and
-// the result rounded to fp16 once.
+// fp16(d * (q - 8)) before it is multiplied (the reference kernel's rounding);
+// then the fp32 bias is added, the activation applied in fp32 and the result
+// rounded to fp16 once. Split-K partial sums are reduced in a fixed order, so
+// results are identical run to run.
 //
 // Structure. A 256-thread workgroup (4 waves, 2 x 2) owns a BM x BN output tile
-// and walks K in BK = 32 slices. Each slice of A and B is staged in LDS with K
-// contiguous per row ([m][k] and [n][k]), so every MFMA operand fragment is one
-// 16-byte ds_read. The next slice's global loads are issued into registers
-// before the current slice's MFMAs, then written to the other LDS buffer:
-// one barrier per slice. The B operand arrives in one of four layouts and is
-// converted to [n][k] on its way into LDS:
-//   B_KN  fp16 [K, N] row-major     -- 16-byte loads along n, 2-byte LDS scatter
-//   B_NK  fp16 [N, K] (W^T)         -- 16-byte loads along k, 16-byte LDS writes
-//   B_Q4N q4_0 [K][N/32] 18-byte blocks (32 n at one k) -- dequant + scatter
-//   B_Q4K q4_0 [N][K/32] 18-byte blocks (32 k at one n) -- dequant + 16-byte writes
-// Wave tile (BM/2) x (BN/2) as (BM/64) x (BN/64) MFMA 32x32 tiles.
+// and walks its K range in BK = 64 slices staged in LDS with K contiguous per
+// row ([m][k] and [n][k], rows padded to 144 B so a 16-lane ds_read_b128 phase
+// touches every bank once). The next slice's global loads are issued into
+// registers before the current slice's MFMAs and written to the other LDS
+// buffer afterwards: one barrier per slice. B arrives in one of five layouts
+// and is converted to [n][k] on its way into LDS:
+//   B_KN  fp16 [K, N]                -- 16-byte loads along n, 2-byte LDS scatter
+//   B_NK  fp16 [N, K] (W^T)          -- 16-byte loads and 16-byte LDS writes
+//   B_Q4N q4_0 [K][N/32] 18-B blocks -- dequantize, 2-byte LDS scatter
+//   B_Q4K q4_0 [N][K/32] 18-B blocks -- dequantize, 16-byte LDS writes
 //
-// MFMA operand layout (v_mfma_f32_32x32x16_f16, 64 lanes): lane l supplies row
-// (l % 32) of the A fragment and column (l % 32) of the B fragment, each as 8
-// consecutive k at offset 8 * (l / 32); A and B use the same k assignment, so
-// the contraction is correct for any k permutation within the 16. Result
-// element i of lane l is C[(i/4)*8 + (l/32)*4 + i%4][l % 32].
+// MFMA roles are swapped: the weight fragment is the instruction's A operand
+// and the activation fragment its B operand, so the 32x32 result is C^T and
+// lane l holds, for output row m = l % 32, four runs of 4 consecutive output
+// columns -- stored as 8-byte vectors. (Operand layout of
+// v_mfma_f32_32x32x16_f16: lane l supplies row l % 32 of A and column l % 32
+// of B, each as 8 consecutive k at offset 8 * (l / 32); result element i of
+// lane l is D[(i/4)*8 + (l/32)*4 + i%4][l % 32].)
+//
+// Split-K (small M): gridDim.z = batch * splits; split s writes its fp32
+// partial tile to a library workspace and `splitk_reduce` sums the splits in
+// order 0..S-1, adds bias, applies the activation and rounds.
+#include <atomic>
+#include <mutex>
+#include <vector>
+
 #include "device.h"
 #include "internal.h"
 
 namespace {
 
 constexpr int TPB = 256;
-constexpr int BK = 32;
-constexpr int LDS_STRIDE = BK + 8;  // halves per LDS row: 80 B keeps 16-byte alignment
+constexpr int BK = 64;
+constexpr int LDS_STRIDE = BK + 8;  // halves per LDS row (144 B)
 
 enum BMode { B_KN = 0, B_NK = 1, B_Q4N = 2, B_Q4K = 3 };
 
@@ -42,16 +53,17 @@ struct GemmArgs {
     const f16 *A;
     long long lda, sA;          // row stride, batch stride (elements)
     const void *B;
-    long long ldb, sB;          // fp16: elements; q4: bytes per block row, batch stride bytes
+    long long ldb, sB;          // fp16: elements; q4: bytes per block row / batch stride bytes
     const float *bias;
     f16 *C;
     long long ldc, sC;
     int M, N, K, act;
+    int splits, k_per_split;    // split-K: K range [s*k_per_split, min(K, (s+1)*k_per_split))
+    float *ws;                  // split-K workspace [batch][splits][M][N] fp32
 };
 
 __device__ __forceinline__ f16 q4_val(float d, int q) { return (f16) (d * (float) (q - 8)); }
 
-// Loads 18-byte q4_0 block (2-byte aligned) into d and 16 code bytes.
 __device__ __forceinline__ void load_q4_block(const uint8_t *p, float &d, uint32_t qs[4]) {
     const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
     d = (float) __builtin_bit_cast(f16, h[0]);
@@ -59,47 +71,52 @@ __device__ __forceinline__ void load_q4_block(const uint8_t *p, float &d, uint32
     for (int i = 0; i < 4; ++i) qs[i] = (uint32_t) h[1 + 2 * i] | ((uint32_t) h[2 + 2 * i] << 16);
 }
 
+__device__ __forceinline__ int nib(const uint32_t qs[4], int j, int shift) {
+    return (int) ((qs[j >> 2] >> ((j & 3) * 8 + shift)) & 0xF);
+}
+
 template <int BM, int BN, int MODE, bool AVEC, bool BVEC>
 struct Gemm {
-    static constexpr int TM = BM / 64;   // 32x32 tiles per wave along M
+    static constexpr int TM = BM / 64;   // 32-row MFMA tiles per wave along M
     static constexpr int TN = BN / 64;
-    static constexpr int A_VECS = BM * BK / 8 / TPB;   // 16-byte vectors of A per thread
+    static constexpr int A_VECS = BM * BK / 8 / TPB;
     static constexpr int B_VECS = BN * BK / 8 / TPB;
-    // q4 work items per thread: (block, half) pairs
-    static constexpr int Q4N_ITEMS = (BK * (BN / 32) * 2 + TPB - 1) / TPB;
-    static constexpr int Q4K_ITEMS = (BN * (BK / 32) * 2 + TPB - 1) / TPB;
-    static constexpr int B_ITEMS = (MODE == B_Q4N) ? Q4N_ITEMS : (MODE == B_Q4K) ? Q4K_ITEMS : B_VECS;
+    static constexpr int Q4N_ITEMS_ALL = BK * (BN / 32) * 2;   // (k, block, half)
+    static constexpr int Q4K_ITEMS_ALL = BN * (BK / 32) * 2;   // (n, block, half)
+    static constexpr int Q4N_ITEMS = (Q4N_ITEMS_ALL + TPB - 1) / TPB;
+    static constexpr int Q4K_ITEMS = (Q4K_ITEMS_ALL + TPB - 1) / TPB;
+    static constexpr int B_ITEMS = MODE == B_Q4N ? Q4N_ITEMS : MODE == B_Q4K ? Q4K_ITEMS : B_VECS;
+    static constexpr bool Q4 = MODE == B_Q4N || MODE == B_Q4K;
 
     struct Regs {
         f16x8 a[A_VECS];
-        f16x8 b[B_ITEMS > 0 ? B_ITEMS : 1];
-        float qd[B_ITEMS > 0 ? B_ITEMS : 1];
-        uint32_t qs[B_ITEMS > 0 ? B_ITEMS : 1][4];
+        f16x8 b[Q4 ? 1 : B_ITEMS];
+        float qd[Q4 ? B_ITEMS : 1];
+        uint32_t qs[Q4 ? B_ITEMS : 1][4];
     };
 
-    // ---- global -> registers ----
     static __device__ __forceinline__ void load_a(const GemmArgs &p, const f16 *A, int m0, int k0,
-                                                  Regs &r) {
+                                                  int kend, Regs &r) {
 #pragma unroll
         for (int i = 0; i < A_VECS; ++i) {
             const int v = threadIdx.x + i * TPB;
             const int row = v / (BK / 8), kc = (v % (BK / 8)) * 8;
             const int m = m0 + row, k = k0 + kc;
             if constexpr (AVEC) {
-                r.a[i] = (m < p.M && k < p.K) ? *reinterpret_cast<const f16x8 *>(A + m * p.lda + k)
-                                              : f16x8{};
+                r.a[i] = (m < p.M && k < kend) ? *reinterpret_cast<const f16x8 *>(A + m * p.lda + k)
+                                               : f16x8{};
             } else {
                 f16x8 t;
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    t[j] = (m < p.M && k + j < p.K) ? A[m * p.lda + k + j] : (f16) 0;
+                    t[j] = (m < p.M && k + j < kend) ? A[m * p.lda + k + j] : (f16) 0;
                 r.a[i] = t;
             }
         }
     }
 
     static __device__ __forceinline__ void load_b(const GemmArgs &p, const void *Bv, int n0, int k0,
-                                                  Regs &r) {
+                                                  int kend, Regs &r) {
         if constexpr (MODE == B_KN) {
             const f16 *B = reinterpret_cast<const f16 *>(Bv);
 #pragma unroll
@@ -108,13 +125,13 @@ struct Gemm {
                 const int kr = v / (BN / 8), nc = (v % (BN / 8)) * 8;
                 const int k = k0 + kr, n = n0 + nc;
                 if constexpr (BVEC) {
-                    r.b[i] = (k < p.K && n < p.N) ? *reinterpret_cast<const f16x8 *>(B + k * p.ldb + n)
-                                                  : f16x8{};
+                    r.b[i] = (k < kend && n < p.N) ? *reinterpret_cast<const f16x8 *>(B + k * p.ldb + n)
+                                                   : f16x8{};
                 } else {
                     f16x8 t;
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        t[j] = (k < p.K && n + j < p.N) ? B[k * p.ldb + n + j] : (f16) 0;
+                        t[j] = (k < kend && n + j < p.N) ? B[k * p.ldb + n + j] : (f16) 0;
                     r.b[i] = t;
                 }
             }
@@ -126,18 +143,17 @@ struct Gemm {
                 const int row = v / (BK / 8), kc = (v % (BK / 8)) * 8;
                 const int n = n0 + row, k = k0 + kc;
                 if constexpr (BVEC) {
-                    r.b[i] = (n < p.N && k < p.K) ? *reinterpret_cast<const f16x8 *>(B + n * p.ldb + k)
-                                                  : f16x8{};
+                    r.b[i] = (n < p.N && k < kend) ? *reinterpret_cast<const f16x8 *>(B + n * p.ldb + k)
+                                                   : f16x8{};
                 } else {
                     f16x8 t;
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        t[j] = (n < p.N && k + j < p.K) ? B[n * p.ldb + k + j] : (f16) 0;
+                        t[j] = (n < p.N && k + j < kend) ? B[n * p.ldb + k + j] : (f16) 0;
                     r.b[i] = t;
                 }
             }
         } else if constexpr (MODE == B_Q4N) {
-            // Tile = BK rows (k) x BN/32 blocks. Item = (k, block, half).
             const uint8_t *W = reinterpret_cast<const uint8_t *>(Bv);
 #pragma unroll
             for (int i = 0; i < Q4N_ITEMS; ++i) {
@@ -147,10 +163,10 @@ struct Gemm {
                 const int k = k0 + kr, n = n0 + nb * 32;
                 r.qd[i] = 0.0f;
                 r.qs[i][0] = r.qs[i][1] = r.qs[i][2] = r.qs[i][3] = 0x88888888u;  // q = 8 -> 0
-                if (it < BK * (BN / 32) * 2 && k < p.K && n < p.N)
+                if (it < Q4N_ITEMS_ALL && k < kend && n < p.N)
                     load_q4_block(W + (long long) k * p.ldb + (long long) (n / 32) * 18, r.qd[i], r.qs[i]);
             }
-        } else {  // B_Q4K: tile = BN rows (n) x BK/32 blocks. Item = (n, block, half).
+        } else {
             const uint8_t *W = reinterpret_cast<const uint8_t *>(Bv);
 #pragma unroll
             for (int i = 0; i < Q4K_ITEMS; ++i) {
@@ -160,13 +176,12 @@ struct Gemm {
                 const int n = n0 + nr, k = k0 + kb * 32;
                 r.qd[i] = 0.0f;
                 r.qs[i][0] = r.qs[i][1] = r.qs[i][2] = r.qs[i][3] = 0x88888888u;
-                if (it < BN * (BK / 32) * 2 && n < p.N && k < p.K)
+                if (it < Q4K_ITEMS_ALL && n < p.N && k < kend)
                     load_q4_block(W + (long long) n * p.ldb + (long long) (k / 32) * 18, r.qd[i], r.qs[i]);
             }
         }
     }
 
-    // ---- registers -> LDS ([m][k] and [n][k]) ----
     static __device__ __forceinline__ void store(f16 *As, f16 *Bs, const Regs &r) {
 #pragma unroll
         for (int i = 0; i < A_VECS; ++i) {
@@ -193,31 +208,26 @@ struct Gemm {
 #pragma unroll
             for (int i = 0; i < Q4N_ITEMS; ++i) {
                 const int it = threadIdx.x + i * TPB;
-                if (it >= BK * (BN / 32) * 2) continue;
+                if (it >= Q4N_ITEMS_ALL) continue;
                 const int blk = it >> 1, half = it & 1;
                 const int kr = blk / (BN / 32), nb = blk % (BN / 32);
-                const int shift = half * 4;
                 // byte j: low nibble = element j, high nibble = element j + 16
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int q = (int) ((r.qs[i][j >> 2] >> ((j & 3) * 8 + shift)) & 0xF);
-                    Bs[(nb * 32 + half * 16 + j) * LDS_STRIDE + kr] = q4_val(r.qd[i], q);
-                }
+                for (int j = 0; j < 16; ++j)
+                    Bs[(nb * 32 + half * 16 + j) * LDS_STRIDE + kr] = q4_val(r.qd[i], nib(r.qs[i], j, half * 4));
             }
         } else {
 #pragma unroll
             for (int i = 0; i < Q4K_ITEMS; ++i) {
                 const int it = threadIdx.x + i * TPB;
-                if (it >= BN * (BK / 32) * 2) continue;
+                if (it >= Q4K_ITEMS_ALL) continue;
                 const int blk = it >> 1, half = it & 1;
                 const int nr = blk / (BK / 32), kb = blk % (BK / 32);
-                const int shift = half * 4;
                 f16x8 lo, hi;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    lo[j] = q4_val(r.qd[i], (int) ((r.qs[i][j >> 2] >> ((j & 3) * 8 + shift)) & 0xF));
-                    hi[j] = q4_val(r.qd[i],
-                                   (int) ((r.qs[i][(j + 8) >> 2] >> (((j + 8) & 3) * 8 + shift)) & 0xF));
+                    lo[j] = q4_val(r.qd[i], nib(r.qs[i], j, half * 4));
+                    hi[j] = q4_val(r.qd[i], nib(r.qs[i], j + 8, half * 4));
                 }
                 f16 *dst = Bs + nr * LDS_STRIDE + kb * 32 + half * 16;
                 *reinterpret_cast<f16x8 *>(dst) = lo;
@@ -226,11 +236,14 @@ struct Gemm {
         }
     }
 
-    static __device__ void run(const GemmArgs &p) {
+    // Must inline into the kernel: as a called function it gets a ~1 KB
+    // scratch frame per lane and runs an order of magnitude slower.
+    static __device__ __forceinline__ void run(const GemmArgs &p) {
         __shared__ __attribute__((aligned(16))) f16 As[2][BM * LDS_STRIDE];
         __shared__ __attribute__((aligned(16))) f16 Bs[2][BN * LDS_STRIDE];
 
-        const int bz = blockIdx.z;
+        const int bz = blockIdx.z / p.splits;
+        const int split = blockIdx.z % p.splits;
         const f16 *A = p.A + (long long) bz * p.sA;
         const void *B;
         if constexpr (MODE == B_KN || MODE == B_NK)
@@ -240,63 +253,110 @@ struct Gemm {
         const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+        const int kbeg = split * p.k_per_split;
+        const int kend = min(p.K, kbeg + p.k_per_split);
 
-        f32x16 acc[TM][TN];
+        f32x16 acc[TN][TM];
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+            for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
 
-        const int KT = (p.K + BK - 1) / BK;
+        const int KT = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
         Regs r;
-        load_a(p, A, m0, 0, r);
-        load_b(p, B, n0, 0, r);
-        store(As[0], Bs[0], r);
+        if (KT > 0) {
+            load_a(p, A, m0, kbeg, kend, r);
+            load_b(p, B, n0, kbeg, kend, r);
+            store(As[0], Bs[0], r);
+        }
         __syncthreads();
 
         for (int kt = 0; kt < KT; ++kt) {
             const int cur = kt & 1;
             if (kt + 1 < KT) {
-                load_a(p, A, m0, (kt + 1) * BK, r);
-                load_b(p, B, n0, (kt + 1) * BK, r);
+                load_a(p, A, m0, kbeg + (kt + 1) * BK, kend, r);
+                load_b(p, B, n0, kbeg + (kt + 1) * BK, kend, r);
             }
             const f16 *as = As[cur];
             const f16 *bs = Bs[cur];
 #pragma unroll
             for (int ks = 0; ks < BK; ks += 16) {
-                f16x8 af[TM], bf[TN];
+                f16x8 wf[TN], xf[TM];
                 const int kk = ks + (lane >> 5) * 8;
 #pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    wf[j] = *reinterpret_cast<const f16x8 *>(bs + (wn + j * 32 + (lane & 31)) * LDS_STRIDE + kk);
+#pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    af[i] = *reinterpret_cast<const f16x8 *>(as + (wm + i * 32 + (lane & 31)) * LDS_STRIDE + kk);
+                    xf[i] = *reinterpret_cast<const f16x8 *>(as + (wm + i * 32 + (lane & 31)) * LDS_STRIDE + kk);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    bf[j] = *reinterpret_cast<const f16x8 *>(bs + (wn + j * 32 + (lane & 31)) * LDS_STRIDE + kk);
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    for (int i = 0; i < TM; ++i)
+                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[j][i], 0, 0, 0);
             }
             if (kt + 1 < KT) store(As[cur ^ 1], Bs[cur ^ 1], r);
             __syncthreads();
         }
 
+        // acc[j][i][e]: n = n0 + wn + j*32 + (e/4)*8 + (lane/32)*4 + e%4, m = m0 + wm + i*32 + lane%32
+        if (p.splits > 1) {
+            float *ws = p.ws + ((long long) bz * p.splits + split) * (long long) p.M * p.N;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int m = m0 + wm + i * 32 + (lane & 31);
+                    if (m >= p.M) continue;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int n = n0 + wn + j * 32 + g * 8 + (lane >> 5) * 4;
+                        float *dst = ws + (long long) m * p.N + n;
+                        if (n + 3 < p.N && (p.N & 3) == 0) {
+                            *reinterpret_cast<f32x4 *>(dst) =
+                                f32x4{acc[j][i][g * 4], acc[j][i][g * 4 + 1], acc[j][i][g * 4 + 2], acc[j][i][g * 4 + 3]};
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (n + e < p.N) dst[e] = acc[j][i][g * 4 + e];
+                        }
+                    }
+                }
+            return;
+        }
+
         f16 *C = p.C + (long long) bz * p.sC;
+        const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn + j * 32 + (lane & 31);
-            const float bv = (p.bias && col < p.N) ? p.bias[col] : 0.0f;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn + j * 32 + g * 8 + (lane >> 5) * 4;
+                float bv[4];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-                    if (row < p.M && col < p.N)
-                        C[(long long) row * p.ldc + col] = (f16) apply_act(acc[i][j][e] + bv, p.act);
+                for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int m = m0 + wm + i * 32 + (lane & 31);
+                    if (m >= p.M) continue;
+                    f16 *dst = C + (long long) m * p.ldc + n;
+                    if (vec_store && n + 3 < p.N) {
+                        f16x4 o;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                        *reinterpret_cast<f16x4 *>(dst) = o;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) dst[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                    }
                 }
             }
         }
+    }
+
+    static __device__ __forceinline__ bool hx_aligned8(const void *p) {
+        return (reinterpret_cast<uintptr_t>(p) & 7) == 0;
     }
 };
 
@@ -305,53 +365,427 @@ __global__ __launch_bounds__(TPB) void gemm_kernel(GemmArgs p) {
     Gemm<BM, BN, MODE, AVEC, BVEC>::run(p);
 }
 
+// ---- W^T fast path: multi-stage direct-to-LDS pipeline -------------------------
+//
+// For B_NK with K % 64 == 0 (every encoder GEMM): each K slice of A and B is
+// copied HBM -> LDS by global_load_lds_dwordx4 (lane i of a wave writes 16 B at
+// the wave's LDS base + 16 i), so a ring of STAGES slices can be in flight
+// without holding any of it in registers. LDS rows are 128 B (64 halves),
+// unpadded; 16-byte chunk c of row r is stored in slot c ^ ((r >> 1) & 7) --
+// the swizzle is applied by choosing which chunk each lane loads, and it makes
+// the 16 rows one ds_read_b128 phase touches land in 16 distinct bank groups.
+// Rows past M or N are loaded from a clamped (valid) row and never stored.
+// Each stage is its own __shared__ array so the compiler can tell the in-flight
+// copies apart from the slice being read.
+constexpr int DS_ROW = 64;  // halves per LDS row (128 B)
+
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+template <int ROWS>
+__device__ __forceinline__ void lds_copy_slice(const f16 *__restrict__ base, long long ld, int row0,
+                                               int rows_valid, int k0, f16 *lds) {
+    // ROWS x 64 halves: ROWS/8 wave-instructions, dealt round-robin to the 4 waves.
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < ROWS / 32; ++j) {
+        const int rg = j * 4 + wave;                 // 8-row group
+        const int r = rg * 8 + (lane >> 3);          // row within the slice
+        const int slot = lane & 7;
+        const int c = slot ^ swz(r);
+        int gr = row0 + r;
+        gr = gr < rows_valid ? gr : rows_valid - 1;  // clamp: never read out of bounds
+        const f16 *src = base + (long long) gr * ld + k0 + c * 8;
+        // Issued through asm so the compiler does not treat the copy as an
+        // LDS store aliasing every later ds_read (it would wait vmcnt(0) and
+        // drain the ring); the kernel's explicit vmcnt waits order it instead.
+        const uint32_t dst = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) f16 *) (lds + rg * 8 * DS_ROW);
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                     :
+                     : "v"(src), "s"(__builtin_amdgcn_readfirstlane(dst))
+                     : "memory", "m0");
+    }
+}
+
+template <int BM, int BN>
+__device__ __forceinline__ f16 *stage_a(int s, f16 *a0, f16 *a1, f16 *a2, f16 *a3) {
+    return s == 0 ? a0 : s == 1 ? a1 : s == 2 ? a2 : a3;
+}
+
+// s_waitcnt encoding (gfx9): vmcnt in [3:0] and [15:14]; expcnt/lgkmcnt left at max.
+#define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+template <int BM, int BN, int STAGES>
+__global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
+    constexpr int TM = BM / 64, TN = BN / 64;
+    constexpr int LOADS = BM / 32 + BN / 32;     // wave-instructions per slice per wave
+    __shared__ __attribute__((aligned(16))) f16 sA0[BM * DS_ROW], sB0[BN * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 sA1[BM * DS_ROW], sB1[BN * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 sA2[STAGES > 2 ? BM * DS_ROW : 8], sB2[STAGES > 2 ? BN * DS_ROW : 8];
+    __shared__ __attribute__((aligned(16))) f16 sA3[STAGES > 3 ? BM * DS_ROW : 8], sB3[STAGES > 3 ? BN * DS_ROW : 8];
+
+    const int bz = blockIdx.z / p.splits;
+    const int split = blockIdx.z % p.splits;
+    const f16 *A = p.A + (long long) bz * p.sA;
+    const f16 *B = reinterpret_cast<const f16 *>(p.B) + (long long) bz * p.sB;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;   // K range is a multiple of 64
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
+
+    auto issue = [&](int kt, int st) {
+        f16 *a = stage_a<BM, BN>(st, sA0, sA1, sA2, sA3);
+        f16 *b = stage_a<BM, BN>(st, sB0, sB1, sB2, sB3);
+        lds_copy_slice<BM>(A, p.lda, m0, p.M, kbeg + kt * BK, a);
+        lds_copy_slice<BN>(B, p.ldb, n0, p.N, kbeg + kt * BK, b);
+    };
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < KT) issue(s, s);
+
+    for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
+#pragma unroll
+        for (int st = 0; st < STAGES; ++st) {
+            const int kt = kt0 + st;
+            if (kt >= KT) break;
+            // this wave's copies of slice kt are done once at most the later
+            // in-flight slices remain outstanding
+            if (kt + STAGES - 1 <= KT) HX_WAIT_VMCNT(LOADS * (STAGES - 2));
+            else HX_WAIT_VMCNT(0);
+            // A bare barrier, not __syncthreads(): its release fence would wait
+            // for every in-flight copy (vmcnt 0) and drain the ring. Slice kt's
+            // copies are complete per wave (the wait above) and slice kt-1's
+            // LDS reads completed before the MFMAs that consumed them.
+            __builtin_amdgcn_s_barrier();
+            if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (st + STAGES - 1) % STAGES);
+            const f16 *as = stage_a<BM, BN>(st, sA0, sA1, sA2, sA3);
+            const f16 *bs = stage_a<BM, BN>(st, sB0, sB1, sB2, sB3);
+#pragma unroll
+            for (int ks = 0; ks < BK; ks += 16) {
+                const int c = (ks >> 3) + (lane >> 5);   // 16-byte chunk of this lane's 8 k
+                f16x8 wf[TN], xf[TM];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int r = wn + j * 32 + (lane & 31);
+                    wf[j] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int r = wm + i * 32 + (lane & 31);
+                    xf[i] = *reinterpret_cast<const f16x8 *>(as + r * DS_ROW + ((c ^ swz(r)) << 3));
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+            }
+        }
+    }
+
+    // epilogue: identical to Gemm::run's
+    if (p.splits > 1) {
+        float *ws = p.ws + ((long long) bz * p.splits + split) * (long long) p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int m = m0 + wm + i * 32 + (lane & 31);
+                if (m >= p.M) continue;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = n0 + wn + j * 32 + g * 8 + (lane >> 5) * 4;
+                    float *dst = ws + (long long) m * p.N + n;
+                    if (n + 3 < p.N && (p.N & 3) == 0) {
+                        *reinterpret_cast<f32x4 *>(dst) =
+                            f32x4{acc[j][i][g * 4], acc[j][i][g * 4 + 1], acc[j][i][g * 4 + 2], acc[j][i][g * 4 + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) dst[e] = acc[j][i][g * 4 + e];
+                    }
+                }
+            }
+        return;
+    }
+    f16 *C = p.C + (long long) bz * p.sC;
+    const bool vec_store = (p.ldc & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int n = n0 + wn + j * 32 + g * 8 + (lane >> 5) * 4;
+            float bv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int m = m0 + wm + i * 32 + (lane & 31);
+                if (m >= p.M) continue;
+                f16 *dst = C + (long long) m * p.ldc + n;
+                if (vec_store && n + 3 < p.N) {
+                    f16x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                    *reinterpret_cast<f16x4 *>(dst) = o;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < p.N) dst[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                }
+            }
+        }
+    }
+}
+
+// Sums S fp32 partials in order 0..S-1, adds bias, applies the activation and
+// rounds once; 4 consecutive outputs per thread.
+__global__ __launch_bounds__(TPB) void splitk_reduce(const float *__restrict__ ws,
+                                                     const float *__restrict__ bias,
+                                                     f16 *__restrict__ C, long long ldc, long long sC,
+                                                     int M, int N, int splits, int act, int batch) {
+    const long long per = (long long) M * N;
+    const long long quads = (per + 3) / 4;
+    const long long total = quads * batch;
+    const long long stride = (long long) gridDim.x * TPB;
+    for (long long q = (long long) blockIdx.x * TPB + threadIdx.x; q < total; q += stride) {
+        const int bz = (int) (q / quads);
+        const long long idx = (q % quads) * 4;
+        const float *src = ws + (long long) bz * splits * per;
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        const bool vec = (N & 3) == 0;
+        for (int sp = 0; sp < splits; ++sp) {
+            const float *p = src + sp * per + idx;
+            if (vec) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
+                s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
+            } else {
+                for (int e = 0; e < 4; ++e)
+                    if (idx + e < per) s[e] += p[e];
+            }
+        }
+        for (int e = 0; e < 4; ++e) {
+            const long long o = idx + e;
+            if (o >= per) break;
+            const int m = (int) (o / N), n = (int) (o % N);
+            const float b = bias ? bias[n] : 0.0f;
+            C[(long long) bz * sC + (long long) m * ldc + n] = (f16) apply_act(s[e] + b, act);
+        }
+    }
+}
+
+// ---- host side ------------------------------------------------------------------
+
+struct Tile {
+    int bm, bn;
+};
+
+// Split-K workspace: grow-only per device, never freed while the process runs
+// (captured graphs may still reference an older buffer).
+struct Workspace {
+    std::mutex mu;
+    void *ptr[16] = {};
+    size_t size[16] = {};
+    size_t want[16] = {};
+};
+Workspace g_ws;
+
+int current_device() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 16) d = 0;
+    return d;
+}
+
+// Workspace for `bytes`, or nullptr when it cannot be provided without an
+// allocation during stream capture (the caller then runs without split-K).
+float *workspace(size_t bytes) {
+    const int d = current_device();
+    std::lock_guard<std::mutex> g(g_ws.mu);
+    if (g_ws.size[d] >= bytes) return static_cast<float *>(g_ws.ptr[d]);
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(hx::stream(), &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+        return nullptr;
+    void *p = nullptr;
+    const size_t sz = bytes < ((size_t) 64 << 20) ? ((size_t) 64 << 20) : bytes;
+    if (hipMalloc(&p, sz) != hipSuccess) return nullptr;
+    g_ws.ptr[d] = p;   // the previous buffer is intentionally kept alive
+    g_ws.size[d] = sz;
+    return static_cast<float *>(p);
+}
+
+// Chooses the tile and split count: fewest "waves" of workgroups over the
+// 256 CUs, weighted by a per-tile efficiency, and split-K only when the
+// tiles alone leave most CUs idle.
+void plan_tiles(long long M, long long N, long long K, int batch, Tile &t, int &splits) {
+    static const Tile cands[] = {{256, 128}, {128, 128}, {64, 64}};
+    static const double eff[] = {0.92, 0.8, 0.45};
+    constexpr int CUS = 256;
+    double best = 1e300;
+    t = {64, 64};
+    splits = 1;
+    for (int c = 0; c < 3; ++c) {
+        const long long tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn) * batch;
+        const long long kt = (K + BK - 1) / BK;
+        for (int s = 1; s <= 16; s *= 2) {
+            if (s > 1 && (kt / s < 2 || tiles * (s / 2) >= CUS)) break;
+            const long long wgs = tiles * s;
+            const long long waves = (wgs + CUS - 1) / CUS;
+            const double cost = (double) waves * cands[c].bm * cands[c].bn * (double) (kt / s + 1) / eff[c]
+                                + (s > 1 ? 2.0 * cands[c].bm * cands[c].bn : 0.0);
+            if (cost < best) {
+                best = cost;
+                t = cands[c];
+                splits = s;
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int MODE>
 void launch_tile(const GemmArgs &p, int batch, bool avec, bool bvec) {
-    dim3 grid((unsigned) ((p.N + BN - 1) / BN), (unsigned) ((p.M + BM - 1) / BM), (unsigned) batch);
+    dim3 grid((unsigned) ((p.N + BN - 1) / BN), (unsigned) ((p.M + BM - 1) / BM),
+              (unsigned) (batch * p.splits));
     if (avec && bvec) HX_LAUNCH((gemm_kernel<BM, BN, MODE, true, true>), grid, dim3(TPB), 0, p);
     else if (avec) HX_LAUNCH((gemm_kernel<BM, BN, MODE, true, false>), grid, dim3(TPB), 0, p);
     else if (bvec) HX_LAUNCH((gemm_kernel<BM, BN, MODE, false, true>), grid, dim3(TPB), 0, p);
     else HX_LAUNCH((gemm_kernel<BM, BN, MODE, false, false>), grid, dim3(TPB), 0, p);
 }
 
+// Tuning override (hexlib_gpu_gemm_override): a tile and/or split count that
+// replaces the heuristic's choice for every later GEMM in the process.
+std::atomic<int> g_ov_bm{0}, g_ov_bn{0}, g_ov_splits{0}, g_ov_path{0};
+
 template <int MODE>
-void launch(const GemmArgs &p, int batch, bool avec, bool bvec) {
-    // 128x128 tiles once there are enough of them to cover the 256 CUs;
-    // 64x64 tiles otherwise (4x the workgroups for small M or N).
-    const long long big = (long long) ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (big >= 256) launch_tile<128, 128, MODE>(p, batch, avec, bvec);
+void launch(GemmArgs p, int batch, bool avec, bool bvec) {
+    Tile t;
+    int splits;
+    plan_tiles(p.M, p.N, p.K, batch, t, splits);
+    if (const int bm = g_ov_bm.load()) t = {bm, g_ov_bn.load()};
+    if (const int s = g_ov_splits.load()) splits = s;
+    p.splits = 1;
+    p.k_per_split = p.K;
+    p.ws = nullptr;
+    if (splits > 1) {
+        const int kt = (p.K + BK - 1) / BK;
+        const int per = (kt + splits - 1) / splits;
+        splits = (kt + per - 1) / per;
+        const size_t bytes = (size_t) batch * splits * (size_t) p.M * p.N * sizeof(float);
+        float *ws = hx::dry_run() ? nullptr : workspace(bytes);
+        if (hx::dry_run()) hx_reserve_workspace(bytes);
+        if (ws || hx::dry_run()) {
+            p.splits = splits;
+            p.k_per_split = per * BK;
+            p.ws = ws;
+        }
+    }
+    bool lds_direct = MODE == B_NK && p.K % BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
+                      avec && bvec && p.k_per_split % BK == 0;
+    if (g_ov_path.load() == 1) lds_direct = false;
+    if (lds_direct) {
+        dim3 grid((unsigned) ((p.N + t.bn - 1) / t.bn), (unsigned) ((p.M + t.bm - 1) / t.bm),
+                  (unsigned) (batch * p.splits));
+        if (t.bm == 256) HX_LAUNCH((gemm_nk_lds<256, 128, 3>), grid, dim3(TPB), 0, p);
+        else if (t.bm == 128) HX_LAUNCH((gemm_nk_lds<128, 128, 2>), grid, dim3(TPB), 0, p);
+        else HX_LAUNCH((gemm_nk_lds<64, 64, 4>), grid, dim3(TPB), 0, p);
+    } else if (t.bm == 256) launch_tile<256, 128, MODE>(p, batch, avec, bvec);
+    else if (t.bm == 128) launch_tile<128, 128, MODE>(p, batch, avec, bvec);
     else launch_tile<64, 64, MODE>(p, batch, avec, bvec);
+    if (p.splits > 1) {
+        const long long quads = ((long long) p.M * p.N + 3) / 4 * batch;
+        HX_LAUNCH(splitk_reduce, dim3(hx::blocks_for(quads, TPB, 4096)), dim3(TPB), 0,
+                  (const float *) p.ws, p.bias, p.C, p.ldc, p.sC, p.M, p.N, p.splits, p.act, batch);
+    }
 }
 
 bool dims_ok(int M, int K, int N, int batch) {
     return M > 0 && K > 0 && N > 0 && batch > 0 && batch <= 65535 && (M + 63) / 64 <= 65535;
 }
 
+GemmArgs args(const hexlib_hf *a, long long lda, long long sA, const void *b, long long ldb,
+              long long sB, const float *bias, hexlib_hf *c, long long ldc, long long sC, int M,
+              int N, int K, int act) {
+    GemmArgs p{};
+    p.A = reinterpret_cast<const f16 *>(a);
+    p.lda = lda;
+    p.sA = sA;
+    p.B = b;
+    p.ldb = ldb;
+    p.sB = sB;
+    p.bias = bias;
+    p.C = reinterpret_cast<f16 *>(c);
+    p.ldc = ldc;
+    p.sC = sC;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.act = act;
+    return p;
+}
+
 }  // namespace
+
+// Dry-run hook: the largest split-K workspace a validated blob will need, so
+// the session can allocate it before capturing a graph.
+static size_t g_reserve = 0;
+void hx_reserve_workspace(size_t bytes) {
+    if (bytes > g_reserve) g_reserve = bytes;
+}
+
+namespace hx {
+int prepare_workspace() {
+    const size_t want = g_reserve;
+    if (!want) return 0;
+    return workspace(want) ? 0 : -1;
+}
+}  // namespace hx
+
+extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
+    const bool tile_ok = (bm == 0 && bn == 0) || (bm == 256 && bn == 128) ||
+                         (bm == 128 && bn == 128) || (bm == 64 && bn == 64);
+    if (!tile_ok || splits < 0 || splits > 64 || path < 0 || path > 2) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+    g_ov_bm = bm;
+    g_ov_bn = bn;
+    g_ov_splits = splits;
+    g_ov_path = path;
+    return HEXLIB_DSP_OK;
+}
 
 extern "C" void matmul_fp16(const hexlib_hf *A, const hexlib_hf *B, hexlib_hf *C, int Bn, int M,
                             int K, int N) {
     if (!A || !B || !C || !dims_ok(M, K, N, Bn)) return;
-    GemmArgs p{reinterpret_cast<const f16 *>(A), K, (long long) M * K, B, N, (long long) K * N,
-               nullptr, reinterpret_cast<f16 *>(C), N, (long long) M * N, M, N, K, 0};
-    launch<B_KN>(p, Bn, K % 8 == 0 && hx::aligned(A, 16), N % 8 == 0 && hx::aligned(B, 16));
+    launch<B_KN>(args(A, K, (long long) M * K, B, N, (long long) K * N, nullptr, C, N,
+                      (long long) M * N, M, N, K, 0),
+                 Bn, K % 8 == 0 && hx::aligned(A, 16), N % 8 == 0 && hx::aligned(B, 16));
 }
 
 extern "C" void matmul_epilogue_f16w_fp16(const hexlib_hf *a, const hexlib_hf *w, const float *bias,
                                           hexlib_hf *out, int M, int K, int N, int act) {
     if (!a || !w || !out || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
-    GemmArgs p{reinterpret_cast<const f16 *>(a), K, 0, w, N, 0, bias,
-               reinterpret_cast<f16 *>(out), N, 0, M, N, K, act};
-    launch<B_KN>(p, 1, K % 8 == 0 && hx::aligned(a, 16), N % 8 == 0 && hx::aligned(w, 16));
+    launch<B_KN>(args(a, K, 0, w, N, 0, bias, out, N, 0, M, N, K, act), 1,
+                 K % 8 == 0 && hx::aligned(a, 16), N % 8 == 0 && hx::aligned(w, 16));
+}
+
+extern "C" void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
+                                           hexlib_hf *out, int M, int K, int N, int act) {
+    if (!a || !wt || !out || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
+    launch<B_NK>(args(a, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act), 1,
+                 K % 8 == 0 && hx::aligned(a, 16), K % 8 == 0 && hx::aligned(wt, 16));
 }
 
 extern "C" void matmul_epilogue_fp16(const hexlib_hf *a, const unsigned char *w, const float *bias,
                                      hexlib_hf *out, int M, int K, int N, int act) {
     if (!a || !w || !out || !dims_ok(M, K, N, 1) || N % 32 || act < 0 || act > 2) return;
     if (!hx::aligned(w, 2)) return;
-    GemmArgs p{reinterpret_cast<const f16 *>(a), K, 0, w, (long long) (N / 32) * 18, 0, bias,
-               reinterpret_cast<f16 *>(out), N, 0, M, N, K, act};
-    launch<B_Q4N>(p, 1, K % 8 == 0 && hx::aligned(a, 16), false);
+    launch<B_Q4N>(args(a, K, 0, w, (long long) (N / 32) * 18, 0, bias, out, N, 0, M, N, K, act), 1,
+                  K % 8 == 0 && hx::aligned(a, 16), false);
 }
 
 extern "C" void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
@@ -359,7 +793,6 @@ extern "C" void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char
                                          int act) {
     if (!a || !wt || !out || !dims_ok(M, K, N, 1) || K % 32 || act < 0 || act > 2) return;
     if (!hx::aligned(wt, 2)) return;
-    GemmArgs p{reinterpret_cast<const f16 *>(a), K, 0, wt, (long long) (K / 32) * 18, 0, bias,
-               reinterpret_cast<f16 *>(out), N, 0, M, N, K, act};
-    launch<B_Q4K>(p, 1, K % 8 == 0 && hx::aligned(a, 16), false);
+    launch<B_Q4K>(args(a, K, 0, wt, (long long) (K / 32) * 18, 0, bias, out, N, 0, M, N, K, act), 1,
+                  K % 8 == 0 && hx::aligned(a, 16), false);
 }

@@ -17,6 +17,10 @@ void note(hipError_t e);
 bool dry_run();
 void set_dry_run(bool on);
 
+// Allocates the largest split-K workspace recorded by dry runs (hipMalloc,
+// outside any capture). 0 on success.
+int prepare_workspace();
+
 inline bool aligned(const void *p, uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
@@ -29,6 +33,9 @@ inline unsigned blocks_for(long long work, int per_block, unsigned cap = 1u << 2
 }
 
 }  // namespace hx
+
+// Records, during a dry run, the split-K workspace a launch would need.
+void hx_reserve_workspace(size_t bytes);
 
 // Every launch goes through here: skipped under a dry run, error recorded.
 #define HX_LAUNCH(kernel, grid, block, lds, ...)                                  \

@@ -438,6 +438,7 @@ int hexlib_gpu_invoke(hexlib_gpu_ctx *ctx, const uint8_t *batch, uint32_t len, u
                 DryScope dry_scope(true);
                 status = run_ops(ctx, batch, hdr, results, done, false);
             }
+            if (status == HEXLIB_DSP_OK && hx::prepare_workspace() != 0) status = HEXLIB_DSP_ERR_INTERNAL;
             if (status == HEXLIB_DSP_OK) {
                 StreamScope ss(ctx->stream);
                 hexlib_gpu_take_error();

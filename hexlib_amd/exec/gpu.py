@@ -202,7 +202,8 @@ class GpuBackend:
                     data = pack_q4_0_kgrouped(arr) if lays[i] == "q4_0_kgroup" else pack_q4_0_nblocked(arr)
             else:
                 arr = np.ascontiguousarray(a, dtype=np.float16 if dt == "fp16" else np.float32)
-                data, shape = arr.tobytes(), arr.shape
+                shape = arr.shape
+                data = (np.ascontiguousarray(arr.T) if lays[i] == "col_major" else arr).tobytes()
             off = len(payload)
             tensors.append(wire.TensorDesc(0, off, len(data), dt, lays[i], wire.pad_ne(shape)))
             shapes.append(tuple(shape))

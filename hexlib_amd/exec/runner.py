@@ -11,7 +11,7 @@ layouts. The C entry adapters are generated from this table
 Ids 1-12 are the reference's and never move. Appended for this build:
 13 rmsnorm, 14 matmul_epilogue_f16w (fp16 weight), 15 matmul_epilogue_q4k
 (q4_0 grouped along K of W^T), 16 transpose_bth (perm (0,2,1,3), the batched
-form of transpose_th).
+form of transpose_th), 17 matmul_epilogue_f16wt (fp16 weight stored W^T).
 
 Each spec also names `extents`: the minimum element count of every buffer as a
 C expression in the scalar names. The generated entry refuses a batch whose
@@ -45,6 +45,7 @@ KIND_ID: dict[str, int] = {
     "matmul_epilogue_f16w": 14,
     "matmul_epilogue_q4k": 15,
     "transpose_bth": 16,
+    "matmul_epilogue_f16wt": 17,
 }
 
 
@@ -217,6 +218,13 @@ SPECS: dict[str, RunnerSpec] = {
         _MM_SCALARS, extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
         weight=(1, "fp16"), primary=False,
         notes="fp16 weight [K, N] row-major"),
+    "matmul_epilogue_f16wt": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_f16wt_fp16", ("fp16", "fp16", "fp32"), "fp16",
+        _MM_SCALARS,
+        layouts=("row_major", "col_major", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
+        weight=(1, "fp16"), primary=False,
+        notes="fp16 weight, logical [K, N] on the wire, stored as W^T [N, K] (K contiguous)"),
     "softmax": RunnerSpec(
         "softmax", "softmax_fp16", ("fp16",), "fp16",
         (_S("rows:0:2", "R"), _S("dim:0:2", "C")), requires=(("axis", -1),),
@@ -268,6 +276,12 @@ def select(kind: str, attrs: Mapping[str, Any], in_dtypes: Sequence[str] | None 
         primary = [(n, s) for n, s in ok if s.primary]
         if len(primary) == 1:
             ok = primary
+    if len(ok) > 1:
+        # same weight dtype, several storage layouts: the plain row-major ABI
+        plain = [(n, s) for n, s in ok
+                 if s.weight is not None and s.buf_layouts()[s.weight[0]] == "row_major"]
+        if len(plain) == 1:
+            ok = plain
     if len(ok) == 1:
         return ok[0]
     if not ok:

@@ -4,9 +4,12 @@ Restates `build_whole_plan_batch` (`hexlib/exec/wholeplan.py:92-357`): every
 tensor lives in a single buffer (fd 0) split into regions --
 
   const  every weight, bias and table, each at its own offset;
-  act    every activation at its own offset (no liveness reuse: HBM is 288 GB,
-         and a non-aliased arena is the configuration the reference runs by
-         default, `alias_activations=False`);
+  act    activations. By default (`reuse=True`) tensors whose lifetimes do
+         not overlap share addresses (lifetimes taken over reshape-unified
+         storage owners), which keeps the working set cache-resident and the
+         batch-32 arena inside the wire's 32-bit offsets; `reuse=False` gives
+         every activation its own offset, the reference's default
+         (`alias_activations=False`) and the control case;
   io     the graph input and output.
 
 A reshape emits no op: its output is placed at its input's offset with its own
@@ -14,7 +17,8 @@ extents. The variant for each op is chosen on the host (`runner.select`) from
 its attrs and input dtypes, and each tensor's bytes take the dtype and layout
 the consuming spec declares (the fp32 pos_embed is staged as fp16; a q4_0
 weight is quantized here, blocked along N or grouped along K per the chosen
-layout). Offsets are 256-byte aligned so every kernel's vector path applies.
+layout; an fp16 weight is stored transposed, `col_major`, by default).
+Offsets are 256-byte aligned so every kernel's vector path applies.
 
 The plan order is the fused graph's op order (a valid topological order; with
 no aliasing the result does not depend on which one).
@@ -74,15 +78,59 @@ class WholePlanBatch:
 
 
 def _spec_for(op, graph: Graph, weight_layout: str | None) -> tuple[str, RunnerSpec]:
+    """`weight_layout="auto"` stores fp16 weights transposed (col_major: both
+    GEMM operands K-contiguous, the fast path) and q4_0 weights in the
+    reference's N-blocked layout; any other value is passed to `select`."""
     dtypes = [graph.tensor(n).dtype for n in op.inputs]
-    name, spec = select(op.kind, dict(op.attrs), dtypes, weight_layout)
+    layout = weight_layout
+    if weight_layout == "auto":
+        layout = "col_major" if op.kind == "matmul_epilogue" and dtypes[1] == "fp16" else None
+    name, spec = select(op.kind, dict(op.attrs), dtypes, layout)
     spec.check_requires(dict(op.attrs))
     return name, spec
 
 
+def _reuse_offsets(g: Graph, acts, reshape_src, owner, wbytes) -> tuple[dict[str, int], int]:
+    """Activation offsets that share memory between tensors whose lifetimes do
+    not overlap. Lifetimes are computed on storage owners, so a reshape's
+    consumers keep its input alive -- the reshape chain is unified BEFORE
+    allocation, which is what the reference's slot reuse lacked
+    (`hexlib/exec/wholeplan.py:235-252, 369-409`). Largest-first placement at
+    the lowest free address, like the reference's VTCM allocator
+    (`hexlib/graph/vtcm.py:83-151`); lifetimes are inclusive at both ends."""
+    first: dict[str, int] = {}
+    last: dict[str, int] = {}
+    act_set = set(acts)
+    for i, op in enumerate(g.ops):
+        for n in op.outputs:
+            o = owner(n)
+            if o in act_set:
+                first.setdefault(o, i)
+                last[o] = max(last.get(o, i), i)
+        for n in op.inputs:
+            o = owner(n)
+            if o in act_set:
+                last[o] = max(last.get(o, i), i)
+    placed: list[tuple[int, int, int, int]] = []   # (offset, end, first, last)
+    offsets: dict[str, int] = {}
+    for n in sorted(acts, key=lambda n: (-wbytes(n), n)):
+        size = align_up(wbytes(n))
+        f, l = first.get(n, 0), last.get(n, len(g.ops))
+        clash = sorted((o, e) for o, e, f2, l2 in placed if f <= l2 and f2 <= l)
+        off = 0
+        for o, e in clash:
+            if off + size <= o:
+                break
+            off = max(off, e)
+        offsets[n] = off
+        placed.append((off, off + size, f, l))
+    span = max((e for _, e, _, _ in placed), default=0)
+    return offsets, span
+
+
 def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
-                           weight_layout: str | None = None, fuse_first: bool = True,
-                           fd: int = 0) -> WholePlanBatch:
+                           weight_layout: str | None = "auto", fuse_first: bool = True,
+                           fd: int = 0, reuse: bool = True) -> WholePlanBatch:
     g = fuse(graph) if fuse_first else graph
     tensors = g.tensors
     io = set(g.inputs) | set(g.outputs)
@@ -148,9 +196,15 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
     retyped = [n for n in acts if wdtype(n) != tensors[n].dtype]
     if retyped:
         raise WholePlanError(f"activations staged in another dtype than declared: {retyped[:6]}")
-    for n in sorted(acts):
-        place(n, cursor, "act")
-        cursor = align_up(cursor + wbytes(n))
+    if reuse:
+        offsets, span = _reuse_offsets(g, acts, reshape_src, owner, wbytes)
+        for n in sorted(acts):
+            place(n, const_end + offsets[n], "act")
+        cursor = align_up(const_end + span)
+    else:
+        for n in sorted(acts):
+            place(n, cursor, "act")
+            cursor = align_up(cursor + wbytes(n))
     for n in sorted(io):
         place(n, cursor, "io")
         cursor = align_up(cursor + wbytes(n))
@@ -178,6 +232,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                 data = pack_q4_0_kgrouped(np.asarray(value))
             else:
                 data = pack_q4_0_nblocked(np.asarray(value))
+        elif p.layout == "col_major":
+            data = np.ascontiguousarray(np.asarray(value, dtype=_NP[p.dtype]).T).tobytes()
         else:
             data = np.ascontiguousarray(np.asarray(value), dtype=_NP[p.dtype]).tobytes()
         if len(data) != p.nbytes:

@@ -9,7 +9,7 @@
  *     dimensions make the call a silent no-op, as in the reference.
  *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
  *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
- *     KIND_ID (1-12) plus appended ids 13-16. Generated from the host's
+ *     KIND_ID (1-12) plus appended ids 13-17. Generated from the host's
  *     RunnerSpec table (hexlib_amd/exec/genentry.py).
  *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
  *     stop/close/hwinfo) that validates a batch blob on the host, resolves
@@ -66,11 +66,13 @@ enum hexlib_dsp_status {
     HEXLIB_DSP_ERR_CACHE = 15
 };
 
-/* Layout ids: hexlib_dsp.h:168-170, plus 3 = q4_0 grouped along K of W^T. */
+/* Layout ids: hexlib_dsp.h:168-170, plus 3 = q4_0 grouped along K of W^T
+ * and 4 = a [K, N] weight stored transposed ([N, K], K contiguous). */
 #define HEXLIB_LAYOUT_ROW_MAJOR     0u
 #define HEXLIB_LAYOUT_TILED_32X32   1u
 #define HEXLIB_LAYOUT_Q4_0_REPACKED 2u
 #define HEXLIB_LAYOUT_Q4_0_KGROUP   3u
+#define HEXLIB_LAYOUT_COL_MAJOR     4u
 
 /* Dtype ids: hexlib/runtime/wire.py:61. */
 #define HEXLIB_DTYPE_FP32  0u
@@ -187,6 +189,12 @@ void patchify_fp32_batched(const float *img, float *out, int BC, int T, int H, i
 void matmul_epilogue_f16w_fp16(const hexlib_hf *a, const hexlib_hf *w,
                                const float *bias, hexlib_hf *out,
                                int M, int K, int N, int act);
+/* act(a @ w + bias), w given transposed: wt fp16 [N, K] (layout col_major of
+ * the logical [K, N] weight; KIND 17). The fast fp16 path: both operands are
+ * K-contiguous. bias may be NULL. */
+void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *wt,
+                                const float *bias, hexlib_hf *out,
+                                int M, int K, int N, int act);
 /* act(a @ deq(w) + bias), w = q4_0 blocks of 32 along K of W^T [N, K] --
  * llama.cpp's native Linear layout (KIND 15). bias may be NULL. */
 void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
@@ -208,6 +216,7 @@ int patchify_fp32_batched_entry(const hexlib_args *a);
 int matmul_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16w_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q4k_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
@@ -221,6 +230,12 @@ void *hexlib_gpu_get_stream(void);
 int   hexlib_gpu_take_error(void);
 const char *hexlib_gpu_error_string(int hip_error);
 const char *hexlib_gpu_status_name(int status);
+/* GEMM tuning override for every later GEMM launch in the process: tile
+ * bm x bn (256x128, 128x128, 64x64; 0x0 = heuristic), split-K count
+ * (0 = heuristic) and W^T code path (0 = automatic, 1 = register-staged,
+ * 2 = direct-to-LDS where its preconditions hold). Returns HEXLIB_DSP_OK or
+ * ERR_INVAL_PARAMS. */
+int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path);
 /* sizeof of each wire struct, in declaration order above (batch_hdr, buf_desc,
  * tensor, op_desc, rsp_hdr, op_result, hexlib_args); returns the count. */
 uint32_t hexlib_gpu_struct_sizes(uint32_t *out, uint32_t cap);

@@ -125,3 +125,43 @@ def test_matmul_epilogue_f16w(dev, M, Kd, N, act, scale):
     got, want = dev.down(do), K.matmul_epilogue_f16w(a, w, bias, act)
     report(f"f16w {M}x{Kd}x{N} act{act}", got, want)
     assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 768, 0), (256, 3072, 768, 0), (256, 768, 3072, 1),
+                                        (8192, 768, 768, 1), (8192, 3072, 768, 0), (8192, 768, 3072, 1),
+                                        (64, 3072, 3072, 2), (784, 768, 768, 0), (17, 40, 24, 2),
+                                        (1, 896, 4864, 0), (300, 200, 136, 1)])
+def test_matmul_epilogue_f16wt(dev, M, Kd, N, act):
+    """fp16 weight stored transposed (W^T [N, K]): the encoder's default GEMM."""
+    r = rng(9)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dw, db, do = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+    dev.check()
+    got, want = dev.down(do), K.matmul_epilogue_f16w(a, w, bias, act)
+    report(f"f16wt {M}x{Kd}x{N} act{act}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("fn", ["matmul_epilogue_f16wt_fp16", "matmul_epilogue_f16w_fp16"])
+def test_split_k_is_deterministic(dev, fn):
+    """M = 256 with K = 3072 runs split-K; the fixed-order reduction must give
+    identical bits on every run."""
+    r = rng(10)
+    M, Kd, N = 256, 3072, 768
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    wdev = np.ascontiguousarray(w.T) if fn.endswith("wt_fp16") else w
+    bias = np.zeros(N, np.float32)
+    da, dw, db = dev.up(a), dev.up(wdev), dev.up(bias)
+    outs = []
+    for _ in range(3):
+        do = dev.empty((M, N), np.float16)
+        getattr(dev.lib, fn)(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, 0)
+        dev.check()
+        outs.append(dev.down(do))
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+    assert K.close_f16(outs[0], K.matmul_epilogue_f16w(a, w, bias, 0), 1e-2, 1e-3).all()

@@ -88,7 +88,7 @@ def test_batched_graph_shapes():
 def test_whole_plan_arena_invariants(cfg):
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg)
-    wb = WP.build_whole_plan_batch(g, feeds)
+    wb = WP.build_whole_plan_batch(g, feeds, reuse=False)
     own = [p for p in wb.placements.values() if p.region != "reshape-alias"]
     spans = sorted((p.offset, p.offset + p.nbytes, p.name) for p in own)
     for (a0, a1, an), (b0, b1, bn) in zip(spans, spans[1:]):
@@ -101,6 +101,46 @@ def test_whole_plan_arena_invariants(cfg):
             assert wb.placements[op.outputs[0]].offset == wb.placements[op.inputs[0]].offset
     assert wb.placements["pos_embed"].dtype == "fp16"
     assert wb.n_ops + wb.skipped_reshapes == len(f.ops)
+
+
+@pytest.mark.parametrize("which", ["tiny", "qwen_b32"])
+def test_reused_arena_never_overlaps_live_tensors(which):
+    """Two activations may share bytes only if no op step sees both alive
+    (lifetimes over reshape-unified owners, inclusive)."""
+    from dataclasses import replace
+    cfg = E.TINY_ENCODER if which == "tiny" else replace(E.QWEN35_VISION_FP16, batch=32)
+    g = E.build_vision_encoder(cfg)
+    f = fuse(g)
+    feeds = {n: np.zeros(t.shape, np.float32) for n, t in f.tensors.items()
+             if t.const or n in f.inputs}
+    wb = WP.build_whole_plan_batch(g, feeds)
+    pl = wb.placements
+    own = {n for n, p in pl.items() if p.region == "act"}
+    alias = {}
+    for op in f.ops:
+        if op.kind == "reshape":
+            alias[op.outputs[0]] = op.inputs[0]
+
+    def owner(n):
+        while n in alias:
+            n = alias[n]
+        return n
+    life = {}
+    for i, op in enumerate(f.ops):
+        for n in op.inputs + op.outputs:
+            o = owner(n)
+            if o in own:
+                a, b = life.get(o, (i, i))
+                life[o] = (min(a, i), max(b, i))
+    names = sorted(own)
+    for i, a in enumerate(names):
+        pa = pl[a]
+        for b in names[i + 1:]:
+            pb = pl[b]
+            if pa.offset < pb.offset + pb.nbytes and pb.offset < pa.offset + pa.nbytes:
+                (fa, la), (fb, lb) = life[a], life[b]
+                assert la < fb or lb < fa, f"{a} and {b} share bytes while both live"
+    assert wb.arena_bytes < 2 ** 32
 
 
 def test_whole_plan_q4_layouts():
