@@ -46,6 +46,7 @@ namespace {
 constexpr int TPB = 256;
 constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // halves per LDS row (144 B)
+constexpr int MAX_SPLITS = 16;      // split-K factor limit (splitk_reduce unrolls to it)
 
 enum BMode { B_KN = 0, B_NK = 1, B_Q4N = 2, B_Q4K = 3 };
 
@@ -375,8 +376,6 @@ __global__ __launch_bounds__(TPB) void gemm_kernel(GemmArgs p) {
 // the swizzle is applied by choosing which chunk each lane loads, and it makes
 // the 16 rows one ds_read_b128 phase touches land in 16 distinct bank groups.
 // Rows past M or N are loaded from a clamped (valid) row and never stored.
-// Each stage is its own __shared__ array so the compiler can tell the in-flight
-// copies apart from the slice being read.
 constexpr int DS_ROW = 64;  // halves per LDS row (128 B)
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
@@ -406,11 +405,6 @@ __device__ __forceinline__ void lds_copy_slice(const f16 *__restrict__ base, lon
     }
 }
 
-template <int BM, int BN>
-__device__ __forceinline__ f16 *stage_a(int s, f16 *a0, f16 *a1, f16 *a2, f16 *a3) {
-    return s == 0 ? a0 : s == 1 ? a1 : s == 2 ? a2 : a3;
-}
-
 // s_waitcnt encoding (gfx9): vmcnt in [3:0] and [15:14]; expcnt/lgkmcnt left at max.
 #define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 
@@ -418,10 +412,9 @@ template <int BM, int BN, int STAGES>
 __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
     constexpr int TM = BM / 64, TN = BN / 64;
     constexpr int LOADS = BM / 32 + BN / 32;     // wave-instructions per slice per wave
-    __shared__ __attribute__((aligned(16))) f16 sA0[BM * DS_ROW], sB0[BN * DS_ROW];
-    __shared__ __attribute__((aligned(16))) f16 sA1[BM * DS_ROW], sB1[BN * DS_ROW];
-    __shared__ __attribute__((aligned(16))) f16 sA2[STAGES > 2 ? BM * DS_ROW : 8], sB2[STAGES > 2 ? BN * DS_ROW : 8];
-    __shared__ __attribute__((aligned(16))) f16 sA3[STAGES > 3 ? BM * DS_ROW : 8], sB3[STAGES > 3 ? BN * DS_ROW : 8];
+    static_assert(STAGES >= 2 && LOADS * (STAGES - 2) <= 63, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(16))) f16 sA[STAGES][BM * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 sB[STAGES][BN * DS_ROW];
 
     const int bz = blockIdx.z / p.splits;
     const int split = blockIdx.z % p.splits;
@@ -441,8 +434,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
         for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
 
     auto issue = [&](int kt, int st) {
-        f16 *a = stage_a<BM, BN>(st, sA0, sA1, sA2, sA3);
-        f16 *b = stage_a<BM, BN>(st, sB0, sB1, sB2, sB3);
+        f16 *a = sA[st];
+        f16 *b = sB[st];
         lds_copy_slice<BM>(A, p.lda, m0, p.M, kbeg + kt * BK, a);
         lds_copy_slice<BN>(B, p.ldb, n0, p.N, kbeg + kt * BK, b);
     };
@@ -466,8 +459,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
             // LDS reads completed before the MFMAs that consumed them.
             __builtin_amdgcn_s_barrier();
             if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (st + STAGES - 1) % STAGES);
-            const f16 *as = stage_a<BM, BN>(st, sA0, sA1, sA2, sA3);
-            const f16 *bs = stage_a<BM, BN>(st, sB0, sB1, sB2, sB3);
+            const f16 *as = sA[st];
+            const f16 *bs = sB[st];
 #pragma unroll
             for (int ks = 0; ks < BK; ks += 16) {
                 const int c = (ks >> 3) + (lane >> 5);   // 16-byte chunk of this lane's 8 k
@@ -561,13 +554,20 @@ __global__ __launch_bounds__(TPB) void splitk_reduce(const float *__restrict__ w
         const long long idx = (q % quads) * 4;
         const float *src = ws + (long long) bz * splits * per;
         float s[4] = {0.f, 0.f, 0.f, 0.f};
-        const bool vec = (N & 3) == 0;
-        for (int sp = 0; sp < splits; ++sp) {
-            const float *p = src + sp * per + idx;
-            if (vec) {
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
-                s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
-            } else {
+        if ((N & 3) == 0) {
+            // all partial loads are issued before the first add (splits <= MAX_SPLITS)
+            f32x4 v[MAX_SPLITS];
+#pragma unroll
+            for (int sp = 0; sp < MAX_SPLITS; ++sp)
+                if (sp < splits) v[sp] = *reinterpret_cast<const f32x4 *>(src + sp * per + idx);
+#pragma unroll
+            for (int sp = 0; sp < MAX_SPLITS; ++sp)
+                if (sp < splits) {
+                    s[0] += v[sp][0]; s[1] += v[sp][1]; s[2] += v[sp][2]; s[3] += v[sp][3];
+                }
+        } else {
+            for (int sp = 0; sp < splits; ++sp) {
+                const float *p = src + sp * per + idx;
                 for (int e = 0; e < 4; ++e)
                     if (idx + e < per) s[e] += p[e];
             }
@@ -621,29 +621,35 @@ float *workspace(size_t bytes) {
     return static_cast<float *>(p);
 }
 
-// Chooses the tile and split count: fewest "waves" of workgroups over the
-// 256 CUs, weighted by a per-tile efficiency, and split-K only when the
-// tiles alone leave most CUs idle.
+// Chooses the tile and split count. Cost = (rounds of workgroups over the 256
+// CUs) x (tile area / per-tile efficiency) x (K slices per split + a per-tile
+// pipeline fill), plus a fixed cost for the reduction launch when K is split.
+// Split-K only while the split grid still fits in one round. The constants
+// come from a sweep of every tile, split and path over the encoder's GEMM
+// shapes on MI355X (within 4% of the best configuration on average).
 void plan_tiles(long long M, long long N, long long K, int batch, Tile &t, int &splits) {
-    static const Tile cands[] = {{256, 128}, {128, 128}, {64, 64}};
-    static const double eff[] = {0.92, 0.8, 0.45};
+    struct Cand { Tile t; double eff, fill; };
+    static const Cand cands[] = {{{128, 128}, 1.0, 10.0}, {{64, 64}, 0.25, 0.0}};
     constexpr int CUS = 256;
+    constexpr double SPLIT_COST = 40000.0;   // the reduction kernel, in the same units
+    const long long kt = (K + BK - 1) / BK;
     double best = 1e300;
     t = {64, 64};
     splits = 1;
-    for (int c = 0; c < 3; ++c) {
-        const long long tiles = ((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn) * batch;
-        const long long kt = (K + BK - 1) / BK;
-        for (int s = 1; s <= 16; s *= 2) {
-            if (s > 1 && (kt / s < 2 || tiles * (s / 2) >= CUS)) break;
-            const long long wgs = tiles * s;
-            const long long waves = (wgs + CUS - 1) / CUS;
-            const double cost = (double) waves * cands[c].bm * cands[c].bn * (double) (kt / s + 1) / eff[c]
-                                + (s > 1 ? 2.0 * cands[c].bm * cands[c].bn : 0.0);
+    for (const Cand &c : cands) {
+        const long long tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn) * batch;
+        for (int s = 1; s <= MAX_SPLITS; s *= 2) {
+            if (s > 1 && (kt / s < 2 || tiles * s > CUS)) break;
+            const long long per = (kt + s - 1) / s;
+            const long long ss = (kt + per - 1) / per;
+            const long long rounds = (tiles * ss + CUS - 1) / CUS;
+            const double area = (double) c.t.bm * c.t.bn;
+            const double cost = (double) rounds * area * ((double) per + c.fill) / c.eff +
+                                (ss > 1 ? SPLIT_COST : 0.0);
             if (cost < best) {
                 best = cost;
-                t = cands[c];
-                splits = s;
+                t = c.t;
+                splits = (int) ss;
             }
         }
     }
@@ -750,7 +756,7 @@ int prepare_workspace() {
 extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
     const bool tile_ok = (bm == 0 && bn == 0) || (bm == 256 && bn == 128) ||
                          (bm == 128 && bn == 128) || (bm == 64 && bn == 64);
-    if (!tile_ok || splits < 0 || splits > 64 || path < 0 || path > 2) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 2) return HEXLIB_DSP_ERR_INVAL_PARAMS;
     g_ov_bm = bm;
     g_ov_bn = bn;
     g_ov_splits = splits;

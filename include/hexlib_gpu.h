@@ -232,9 +232,9 @@ const char *hexlib_gpu_error_string(int hip_error);
 const char *hexlib_gpu_status_name(int status);
 /* GEMM tuning override for every later GEMM launch in the process: tile
  * bm x bn (256x128, 128x128, 64x64; 0x0 = heuristic), split-K count
- * (0 = heuristic) and W^T code path (0 = automatic, 1 = register-staged,
- * 2 = direct-to-LDS where its preconditions hold). Returns HEXLIB_DSP_OK or
- * ERR_INVAL_PARAMS. */
+ * (0 = heuristic, at most 16) and W^T code path (0 = automatic,
+ * 1 = register-staged, 2 = direct-to-LDS where its preconditions hold).
+ * Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
 int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path);
 /* sizeof of each wire struct, in declaration order above (batch_hdr, buf_desc,
  * tensor, op_desc, rsp_hdr, op_result, hexlib_args); returns the count. */

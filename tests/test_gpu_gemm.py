@@ -165,3 +165,55 @@ def test_split_k_is_deterministic(dev, fn):
     for o in outs[1:]:
         np.testing.assert_array_equal(o.view(np.uint16), outs[0].view(np.uint16))
     assert K.close_f16(outs[0], K.matmul_epilogue_f16w(a, w, bias, 0), 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("M,Kd,N", [(256, 768, 768), (300, 320, 138), (33, 1024, 70), (8, 4096, 256)])
+@pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 128)])
+@pytest.mark.parametrize("splits", [2, 5, 16])
+@pytest.mark.parametrize("path", [1, 2])
+def test_forced_tiles_and_splits(dev, M, Kd, N, tile, splits, path):
+    """Every tile, split-K factor and W^T code path, forced through the tuning
+    override, on ragged shapes (M and N not multiples of the tile, N % 4 != 0):
+    in-kernel split-K reduction against the oracle, and bit-identical on a
+    second call (the per-tile arrival counters must be back at zero)."""
+    r = rng(11)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dw, db = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias)
+    assert dev.lib.hexlib_gpu_gemm_override(tile[0], tile[1], splits, path) == 1
+    try:
+        outs = []
+        for act in (1, 1):
+            do = dev.empty((M, N), np.float16)
+            dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+            dev.check()
+            outs.append(dev.down(do))
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    want = K.matmul_epilogue_f16w(a, w, bias, 1)
+    assert K.close_f16(outs[0], want, 1e-2, 1e-3).all()
+    np.testing.assert_array_equal(outs[1].view(np.uint16), outs[0].view(np.uint16))
+
+
+@pytest.mark.parametrize("splits", [3, 8])
+def test_forced_split_batched_matmul(dev, splits):
+    """Split-K on the batched matmul: counters are per (batch, tile)."""
+    r = rng(12)
+    Bn, M, Kd, N = 5, 70, 512, 90
+    a = h16(r.standard_normal((Bn, M, Kd)))
+    b = h16(r.standard_normal((Bn, Kd, N)) / np.sqrt(Kd))
+    da, dbm, do = dev.up(a), dev.up(b), dev.empty((Bn, M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(64, 64, splits, 0) == 1
+    try:
+        dev.lib.matmul_fp16(dev.ptr(da), dev.ptr(dbm), dev.ptr(do), Bn, M, Kd, N)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    assert K.close_f16(dev.down(do), K.matmul_fp16(a, b), 1e-2, 1e-3).all()
+
+
+def test_override_rejects_bad_values(dev):
+    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 3), (256, 256, 0, 0)]:
+        assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
+    assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
