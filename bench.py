@@ -162,6 +162,105 @@ def per_op_in_plan(plan, g, reps: int = 40) -> list[dict]:
     return sorted(rows, key=lambda r: -r["total_us"])
 
 
+# ---- roofline of the dominant kernel ---------------------------------------------------
+
+def dominant_op(g, wb):
+    """The plan's GEMM shape with the most launches per image (ties: first in
+    plan order). For the cfg-4 encoder this is the 256x768x768 W^T linear (QKV
+    thirds, proj, merger input): 49 of the 259 launches."""
+    rows = [(count, -idx, spec, ins, out) for (spec, ins, out), (count, idx, _) in unique_ops(g, wb).items()
+            if spec.startswith("matmul_epilogue")]
+    count, neg_idx, spec, ins, out = max(rows)
+    return {"spec": spec, "index": -neg_idx, "count": count, "inputs": ins, "output": out}
+
+
+def roofline(plan, g, reps: int = 200, iters: int = 7) -> dict:
+    """Algorithmic work of one launch of the dominant op / its mean duration,
+    measured with HIP events on the session stream around a captured graph of
+    `reps` back-to-back launches (cycles_total of a TIMED invoke / reps)."""
+    d = dominant_op(g, plan.batch)
+    shapes = [s for s, _ in d["inputs"]]
+    dtypes = [t for _, t in d["inputs"]]
+    oshape, odt = d["output"]
+    flops = op_work(d["spec"], shapes, oshape, dtypes, odt)[1]
+    nbytes = gemm_bytes(shapes, dtypes, oshape)
+    blob = repeat_op_blob(plan.batch, d["index"], reps)
+    ns = time_blob(plan.session, blob, reps, iters=iters) / reps
+    ridge = MFMA_FP16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    ai = flops / nbytes
+    m, k = shapes[0]
+    n = shapes[1][0] if d["spec"].endswith("f16wt") else shapes[1][-1]
+    out = {"kernel": f"{d['spec']} {m}x{k}x{n}", "launches_per_image": d["count"],
+           "avg_launch_ns": round(ns, 1), "algorithmic_bytes": int(nbytes), "flops": int(flops),
+           "arith_intensity": round(ai, 1)}
+    if ai < ridge:
+        out.update({"bound": "hbm", "achieved": round(nbytes / ns, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(nbytes / ns / HBM_PEAK_GBS, 5)})
+    else:
+        out.update({"bound": "mfma", "achieved": round(flops / ns / 1e3, 3), "peak": MFMA_FP16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(flops / ns / 1e3 / MFMA_FP16_PEAK_TFLOPS, 5)})
+    out["tflops"] = round(flops / ns / 1e3, 3)
+    out["traffic"] = measured_traffic(out["kernel"])
+    return out
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_dominant_gemm.json")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size), when it
+    was taken for this same kernel and shape; else None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t.get("traffic_bytes") if t.get("kernel") == kernel else None
+
+
+def copy_reference(mib: int = 512) -> None:
+    """A plain device copy of known size (mib MiB read + mib MiB written),
+    launched so that a --pmc run can scale FETCH_SIZE/WRITE_SIZE to bytes."""
+    import torch
+    src = torch.ones((mib << 20) // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)    # one elementwise kernel: reads and writes mib MiB
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
+def trace_summary(d: str) -> str:
+    """Markdown summary of a rocprofv3 output directory: per-kernel duration
+    statistics from *_kernel_stats.csv and, for --pmc runs, the mean counter
+    value per dispatch of each kernel from *_counter_collection.csv."""
+    import csv
+    import glob
+    lines = []
+    for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
+        lines += [f"### {os.path.relpath(path, d)}", "",
+                  "| kernel | calls | avg ns | min ns | max ns | % |", "|---|---|---|---|---|---|"]
+        for r in csv.DictReader(open(path)):
+            lines.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']):.0f} | "
+                         f"{r['MinNs']} | {r['MaxNs']} | {float(r['Percentage']):.2f} |")
+        lines.append("")
+    for path in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+        acc = {}
+        for r in csv.DictReader(open(path)):
+            key = (r["Kernel_Name"][:90], r["Counter_Name"], r.get("Grid_Size", ""))
+            a = acc.setdefault(key, [0.0, 0])
+            a[0] += float(r["Counter_Value"])
+            a[1] += 1
+        lines += [f"### {os.path.relpath(path, d)}", "",
+                  "| kernel | grid | counter | dispatches | mean per dispatch |", "|---|---|---|---|---|"]
+        for (k, c, grid), (tot, n) in sorted(acc.items()):
+            lines.append(f"| `{k}` | {grid} | {c} | {n} | {tot / n:.1f} |")
+        lines.append("")
+    return "\n".join(lines)
+
+
 # ---- cold-buffer per-op suite (BASELINE cfg 2 / cfg 3 shapes) -------------------------
 
 def suite_cases():
@@ -320,7 +419,16 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-variants", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="build the plan, launch only the dominant kernel (and, with --copy-ref, a "
+                         "plain copy of known size) and print its roofline object")
+    ap.add_argument("--copy-ref", action="store_true")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="print a markdown summary of a rocprofv3 output directory and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested). Images are independent; see DESIGN.md "
@@ -336,6 +444,14 @@ def main() -> int:
     log("building cfg-4 plan (256x256, batch 1)")
     g, feeds, wb = build_plan(cfg)
     plan = GpuPlan(wb, session)
+    if args.roofline_only:
+        if args.copy_ref:
+            copy_reference()
+        roof = roofline(plan, g)
+        plan.close()
+        session.close()
+        print(json.dumps({"roofline": roof}))
+        return 0
     sec = time_replays(plan, args.steps, args.warmup)
     ms = sec / args.steps * 1e3
     ips = args.steps * cfg.batch / sec
@@ -353,28 +469,15 @@ def main() -> int:
         plan_gpu_ns = rsp.cycles_total
     except Exception as e:  # noqa: BLE001
         log(f"timed graph replay failed: {e}")
-    plan.close()
 
-    # dominant kernel by share of the plan's time
-    dom_spec = {}
-    for r in per_op:
-        d = dom_spec.setdefault(r["op"], {"ns": 0.0, "work": 0.0, "count": 0, "bound": r["bound"]})
-        d["ns"] += r["count"] * r["avg_ns"]
-        d["count"] += r["count"]
-        unit = 1e3 if r["bound"] == "mfma" else 1.0
-        d["work"] += r["count"] * r["avg_ns"] * r["achieved"] * unit
-    dom_name, dom = max(dom_spec.items(), key=lambda kv: kv[1]["ns"])
-    achieved = dom["work"] / dom["ns"]
-    if dom["bound"] == "mfma":
-        roof = {"kernel": dom_name, "bound": "mfma", "achieved": round(achieved / 1e3, 3),
-                "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / 1e3 / MFMA_FP16_PEAK_TFLOPS, 5)}
-    else:
-        roof = {"kernel": dom_name, "bound": "hbm", "achieved": round(achieved, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5)}
-    roof.update({"traffic": None, "launches_per_image": dom["count"],
-                 "avg_launch_ns": round(dom["ns"] / dom["count"], 1),
-                 "share_of_plan": round(dom["ns"] / sum(v["ns"] for v in dom_spec.values()), 3)})
+    roof = roofline(plan, g)
+    share = roof["launches_per_image"] * roof["avg_launch_ns"] / sum(r["count"] * r["avg_ns"] for r in per_op)
+    roof["share_of_plan"] = round(share, 3)
+    top = per_op[0]
+    log(f"roofline: {roof['kernel']} {roof['avg_launch_ns']:.0f} ns/launch, {roof['achieved']} {roof['unit']} "
+        f"({roof['frac'] * 100:.2f}% of {roof['bound']} peak), {share * 100:.1f}% of the plan; "
+        f"largest in-plan row: {top['op']} {top['shape']} {top['total_us']} us")
+    plan.close()
 
     variants = {}
     if not args.no_variants:

@@ -632,6 +632,7 @@ void plan_tiles(long long M, long long N, long long K, int batch, Tile &t, int &
     static const Cand cands[] = {{{128, 128}, 1.0, 10.0}, {{64, 64}, 0.25, 0.0}};
     constexpr int CUS = 256;
     constexpr double SPLIT_COST = 40000.0;   // the reduction kernel, in the same units
+    constexpr int MIN_SPLIT_SLICES = 8;      // shorter K ranges are latency-bound: no gain
     const long long kt = (K + BK - 1) / BK;
     double best = 1e300;
     t = {64, 64};
@@ -639,7 +640,7 @@ void plan_tiles(long long M, long long N, long long K, int batch, Tile &t, int &
     for (const Cand &c : cands) {
         const long long tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn) * batch;
         for (int s = 1; s <= MAX_SPLITS; s *= 2) {
-            if (s > 1 && (kt / s < 2 || tiles * s > CUS)) break;
+            if (s > 1 && (kt / s < MIN_SPLIT_SLICES || tiles * s > CUS)) break;
             const long long per = (kt + s - 1) / s;
             const long long ss = (kt + per - 1) / per;
             const long long rounds = (tiles * ss + CUS - 1) / CUS;
