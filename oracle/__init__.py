@@ -11,10 +11,10 @@ Contents, each citing the reference file it restates:
                 (`hexlib/graph/opdefs/elementwise.py:40-156`, `fused.py:44-53`,
                 `structural.py:55-254`), plus `rmsnorm` from
                 `kernels/rmsnorm_fp16/baseline.c:6-19`.
-* `eager`    -- the fp32 eager oracle (`hexlib/graph/eager.py:32-132`).
-* `interp`   -- the storage-rounding plan executor (`hexlib/exec/interpreter.py:80-205`
-                with `hexlib/exec/vtcm.py:90-146`): fp32 compute, every op output
-                rounded to its declared storage dtype.
+* `eager`    -- `run_fp32`, the fp32 eager oracle (`hexlib/graph/eager.py:32-132`),
+                and `run_stored`, the storage-rounding plan executor
+                (`hexlib/exec/interpreter.py:80-205` with `hexlib/exec/vtcm.py:90-146`):
+                fp32 compute, every op output rounded to its declared storage dtype.
 * `kernels`  -- per-kernel scalar contracts (`kernels/*/baseline.c` +
                 `kernel_api.h`), vectorised in numpy, used by the per-op GPU parity
                 tests.

@@ -268,3 +268,25 @@ def test_nearmiss_gelu_swap_fails():
     good = R.matmul_epilogue_fp16(a, w, bias, 64, 64, 2)
     bad = K.matmul_epilogue_fp16(a, w, bias, 64, 64, 1)
     assert not close(bad, good, 0.01, 3e-4)
+
+
+# ---- extensions: batch axis ------------------------------------------------------
+
+@needs_ref
+def test_transpose_bth_is_per_image_transpose_th():
+    """[B,T,H,D] -> [B,H,T,D] is the reference transpose_th on each image."""
+    x = h(rng(40).standard_normal((3, 8, 5, 16)))
+    got = K.transpose_bth_fp16(x)
+    for b in range(3):
+        np.testing.assert_array_equal(got[b], R.transpose_th_fp16(x[b]))
+
+
+@needs_ref
+def test_batched_patchify_is_per_image_patchify():
+    """A batch stacked on channels ([B*C,T,H,W]) patchifies to the per-image
+    reference outputs stacked along tokens."""
+    B, C, T, H, W, p, m, gh, gw = 3, 3, 1, 64, 64, 16, 2, 4, 4
+    img = rng(41).random((B * C, T, H, W), dtype=np.float32)
+    got = K.patchify_fp32(img, p, m, gh, gw, batch=B)
+    want = np.concatenate([R.patchify_fp32(img[b * C:(b + 1) * C], p, m, gh, gw) for b in range(B)])
+    np.testing.assert_array_equal(got, want)
