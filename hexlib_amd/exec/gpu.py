@@ -233,3 +233,40 @@ class GpuBackend:
         finally:
             self.session.munmap(self._fd)
         return np.frombuffer(raw, dtype=odt).reshape(out_shape), rsp
+
+
+class _Meta:
+    """Shape/dtype stand-in handed to an OpDef's infer."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(shape)
+        self.dtype = dtype
+
+
+def interpreter_backends(gpu: GpuBackend, kinds=None) -> dict:
+    """One plan-executor backend per op kind that has a GPU kernel -- the
+    drop-in for the reference's `interpreter_backends(sim, kinds)`
+    (`hexlib/exec/dsp.py:656-715`): `{kind: backend(arrays, attrs) -> (out,)}`.
+
+    As there, the variant is resolved per call from the op's attrs (`select`),
+    an op no variant accepts is refused, and a dense weight whose spec declares
+    q4_0 is quantized on the way in -- the kernel then multiplies with the 4-bit
+    weight, so an accuracy comparison must be made against the dequantized
+    bytes, not the fp32 original. The output shape comes from the op's infer.
+    """
+    from hexlib_amd.exec.runner import SPECS
+    from hexlib_amd.graph import ops as graph_ops
+
+    available = sorted({spec.kind for spec in SPECS.values()} - {"reshape"})
+    wanted = available if kinds is None else [k for k in kinds if k in available]
+
+    def make(kind: str):
+        def backend(arrays, attrs):
+            metas = [_Meta(np.shape(a), "fp32") for a in arrays]
+            ((out_shape, _),) = graph_ops.get(kind).infer(metas, dict(attrs))
+            out, _ = gpu.run(kind, list(arrays), dict(attrs), tuple(out_shape))
+            return (out,)
+
+        return backend
+
+    return {kind: make(kind) for kind in wanted}

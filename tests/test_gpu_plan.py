@@ -159,3 +159,55 @@ def test_per_op_backend_through_the_wire(session):
     from oracle import kernels as K
     want = K.matmul_epilogue_fp16(a, pack_q4_0_nblocked(w), b, 128, 96, 1)
     assert K.close_f16(y, want, 0.01, 3e-4).all()
+
+
+def test_interpreter_backends_every_kind(session):
+    """The reference-shaped adapter (`interpreter_backends(gpu)[kind](arrays,
+    attrs) -> (out,)`, as `hexlib/exec/dsp.py:656-715` hands to the plan
+    executor) for every kernel kind, fed fp32 arrays like the executor's
+    compute dtype, against the op registry reference on the fp16-rounded
+    inputs the wire carries."""
+    from hexlib_amd import encoder as E
+    from hexlib_amd.exec.gpu import interpreter_backends
+    from oracle import kernels as K
+    from oracle.refs import REFERENCES
+    be = interpreter_backends(GpuBackend(session))
+    r = np.random.default_rng(5)
+
+    def f(*s):
+        return r.standard_normal(s).astype(np.float32)
+
+    def r16(a):
+        return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+    cos, sin = E.rope_tables(E.TINY_ENCODER)
+    T = cos.shape[0]
+    cases = [
+        ("add", [f(64, 96), f(64, 96)], {}, [True, True]),
+        ("scale", [f(12, 64, 32)], {"factor": 0.125}, [True]),
+        ("cast", [f(64, 96)], {"dtype": "fp16"}, [False]),
+        ("softmax", [f(6, 256)], {"axis": -1}, [True]),
+        ("layernorm", [f(16, 768), 1 + 0.02 * f(768), 0.02 * f(768)], {"eps": 1e-6}, [True, False, False]),
+        ("rmsnorm", [f(16, 768), 1 + 0.02 * f(768)], {"eps": 1e-6}, [True, True]),
+        ("rope_2d", [f(T, 2, cos.shape[1]), cos, sin], {}, [True, False, False]),
+        ("transpose", [f(16, 3, 64)], {"perm": (1, 0, 2)}, [True]),
+        ("transpose", [f(6, 40, 24)], {"perm": (0, 2, 1)}, [True]),
+        ("patchify", [r.random((3, 1, 64, 64), dtype=np.float32)],
+         {"patch": 16, "temporal_patch": 1, "merge": 2, "grid_h": 4, "grid_w": 4}, [False]),
+        ("matmul", [f(3, 40, 64), 0.1 * f(3, 64, 48)], {}, [True, True]),
+    ]
+    for kind, arrays, attrs, rounded in cases:
+        (got,) = be[kind](arrays, attrs)
+        ins = [r16(a) if rd else a for a, rd in zip(arrays, rounded)]
+        (want,) = REFERENCES[kind](ins, attrs)
+        want = np.asarray(want, np.float32)
+        exact = kind in ("transpose", "patchify", "cast")
+        if exact:
+            np.testing.assert_array_equal(np.asarray(got, np.float32), want.astype(got.dtype).astype(np.float32))
+        else:
+            assert K.close_f16(got, want.astype(np.float16), 0.02, 2e-3).all(), kind
+    # matmul_epilogue: the dense weight is quantized to q4_0 on the way in
+    a, w, b = f(32, 128), 0.05 * f(128, 64), 0.02 * f(64)
+    (got,) = be["matmul_epilogue"]([a, w, b], {"act": "gelu_tanh"})
+    want = K.matmul_epilogue_fp16(a.astype(np.float16), pack_q4_0_nblocked(w), b, 128, 64, 1)
+    assert K.close_f16(got, want, 0.01, 3e-4).all()
