@@ -3,11 +3,14 @@ roofline fractions and the CPU oracle timed beside it.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-suite]
 
-A step is one whole-plan replay -- the 259-op ViT encoder (BASELINE cfg 4:
-12 blocks, hidden 768, 12 heads, MLP 3072, LayerNorm, 2D RoPE, merger) over one
+A step is one whole-plan replay of the ViT encoder (BASELINE cfg 4: 12
+blocks, hidden 768, 12 heads, MLP 3072, LayerNorm, 2D RoPE, merger) over one
 256x256 image, replayed as ONE captured hipGraph through the session's batch
-invoke. Inputs and weights are resident in HBM before timing starts. `value`
-is images/sec over exactly K replays bracketed by device synchronisation.
+invoke. The plan is the product default: each block's attention chain runs as
+one fused attention op (163 launches); the reference graph's unfused plan (259
+launches) is reported as a variant. Inputs and weights are resident in HBM
+before timing starts. `value` is images/sec over exactly K replays bracketed
+by device synchronisation.
 
 Per-op durations come from the same product path: a blob that repeats one op
 R times, captured as a hipGraph and timed with HIP events on the session
@@ -45,6 +48,7 @@ def log(msg: str) -> None:
 # ---- algorithmic work per op --------------------------------------------------------
 
 _ESZ = {"fp16": 2, "fp32": 4}
+_ATTN_BATCH: dict = {}   # attention input shape -> images per call, filled from the plan
 
 
 def op_work(spec_name: str, in_shapes, out_shape, in_dtypes, out_dtype) -> tuple[str, float]:
@@ -57,6 +61,10 @@ def op_work(spec_name: str, in_shapes, out_shape, in_dtypes, out_dtype) -> tuple
         bn, m, k = in_shapes[0]
         n = in_shapes[1][-1]
         return "mfma", 2.0 * bn * m * k * n
+    if spec_name == "attention":   # q.k^T and p.v over every (image, head); batch from the plan
+        rows, h, d = in_shapes[0]
+        t = rows // max(1, _ATTN_BATCH.get(tuple(in_shapes[0]), 1))
+        return "mfma", 4.0 * rows * t * h * d
     if spec_name.startswith("matmul_epilogue"):
         m, k = in_shapes[0]
         n = in_shapes[1][-1]
@@ -109,6 +117,8 @@ def unique_ops(g, wb):
             continue
         spec = wb.op_specs[i]
         ins = tuple((wb.placements[n].shape, wb.placements[n].dtype) for n in op.inputs)
+        if spec == "attention":
+            _ATTN_BATCH[tuple(ins[0][0])] = int(op.attrs.get("batch", 1))
         o = wb.placements[op.outputs[0]]
         key = (spec, ins, (o.shape, o.dtype))
         if key not in out:
@@ -167,7 +177,7 @@ def per_op_in_plan(plan, g, reps: int = 40) -> list[dict]:
 def dominant_op(g, wb):
     """The plan's GEMM shape with the most launches per image (ties: first in
     plan order). For the cfg-4 encoder this is the 256x768x768 W^T linear (QKV
-    thirds, proj, merger input): 49 of the 259 launches."""
+    thirds, proj, merger input): 49 launches per image."""
     rows = [(count, -idx, spec, ins, out) for (spec, ins, out), (count, idx, _) in unique_ops(g, wb).items()
             if spec.startswith("matmul_epilogue")]
     count, neg_idx, spec, ins, out = max(rows)
@@ -440,8 +450,8 @@ def main() -> int:
     from hexlib_amd.exec.gpu import GpuPlan, GpuSession
 
     session = GpuSession()
-    cfg = E.QWEN35_VISION_FP16
-    log("building cfg-4 plan (256x256, batch 1)")
+    cfg = replace(E.QWEN35_VISION_FP16, attention="fused")
+    log("building cfg-4 plan (256x256, batch 1, fused attention)")
     g, feeds, wb = build_plan(cfg)
     plan = GpuPlan(wb, session)
     if args.roofline_only:
@@ -482,7 +492,9 @@ def main() -> int:
     variants = {}
     if not args.no_variants:
         for label, vcfg, steps in (("256_b32", replace(cfg, batch=32), max(5, args.steps // 10)),
-                                   ("448_b1", E.encoder_at(448), max(10, args.steps // 2))):
+                                   ("448_b1", replace(E.encoder_at(448), attention="fused"),
+                                    max(10, args.steps // 2)),
+                                   ("256_b1_reference_graph", E.QWEN35_VISION_FP16, max(10, args.steps // 2))):
             log(f"variant {label}")
             try:
                 variants[label] = run_variant(session, vcfg, steps, label)
@@ -503,8 +515,10 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: seeded U[0,1] image, N(0,0.02) fp16 weights, random init",
         "config": {"workload": "vit_encoder_256_b1 (BASELINE cfg 4: 12 blocks, hidden 768, "
-                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; 259 ops as one hipGraph)",
-                   "image": 256, "batch": 1, "tokens": 256, "plan_gpu_ns": plan_gpu_ns},
+                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; fused attention, "
+                               f"{wb.n_ops} ops as one hipGraph)",
+                   "image": 256, "batch": 1, "tokens": 256, "attention": "fused",
+                   "plan_ops": wb.n_ops, "plan_gpu_ns": plan_gpu_ns},
         "roofline": roof,
         "cpu_baseline": cpu,
         "per_op_in_plan": per_op,

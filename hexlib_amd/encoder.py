@@ -49,6 +49,7 @@ class VitConfig:
     weight_dtype: str = "fp32"
     norm: str = "layernorm"
     batch: int = 1
+    attention: str = "unfused"   # "fused": one attention op per block (KIND 18)
 
     @property
     def grid(self) -> int:
@@ -209,6 +210,9 @@ def build_vision_encoder(cfg: VitConfig) -> Graph:
                        {"shape": (rows, heads, d)})
             if which in ("q", "k"):
                 t = b.emit("rope_2d", (t, cos, sin), f"{p}.{which}.rope", (rows, heads, d))
+            if cfg.attention == "fused":
+                qkv[which] = t
+                continue
             if B == 1:
                 qkv[which] = b.emit("transpose", (t,), f"{p}.{which}.t", (heads, n, d),
                                     {"perm": (1, 0, 2)})
@@ -219,20 +223,25 @@ def build_vision_encoder(cfg: VitConfig) -> Graph:
                             {"perm": (0, 2, 1, 3)})
                 qkv[which] = b.emit("reshape", (t4,), f"{p}.{which}.t", (B * heads, n, d),
                                     {"shape": (B * heads, n, d)})
-        bh = B * heads
-        qs = b.emit("scale", (qkv["q"],), f"{p}.q.scaled", (bh, n, d),
-                    {"factor": float(d) ** -0.5})
-        ktt = b.emit("transpose", (qkv["k"],), f"{p}.k.tt", (bh, d, n), {"perm": (0, 2, 1)})
-        scores = b.emit("matmul", (qs, ktt), f"{p}.scores", (bh, n, n))
-        probs = b.emit("softmax", (scores,), f"{p}.probs", (bh, n, n), {"axis": -1})
-        ctx = b.emit("matmul", (probs, qkv["v"]), f"{p}.ctx", (bh, n, d))
-        if B == 1:
-            ctxt = b.emit("transpose", (ctx,), f"{p}.ctx.t", (n, heads, d), {"perm": (1, 0, 2)})
+        if cfg.attention == "fused":
+            # one op for the chain below; [rows, heads, d] in and out
+            ctxt = b.emit("attention", (qkv["q"], qkv["k"], qkv["v"]), f"{p}.ctx.t", (rows, heads, d),
+                          {"scale": float(d) ** -0.5, "batch": B})
         else:
-            c4 = b.emit("reshape", (ctx,), f"{p}.ctx.b4", (B, heads, n, d),
-                        {"shape": (B, heads, n, d)})
-            ctxt = b.emit("transpose", (c4,), f"{p}.ctx.t", (B, n, heads, d),
-                          {"perm": (0, 2, 1, 3)})
+            bh = B * heads
+            qs = b.emit("scale", (qkv["q"],), f"{p}.q.scaled", (bh, n, d),
+                        {"factor": float(d) ** -0.5})
+            ktt = b.emit("transpose", (qkv["k"],), f"{p}.k.tt", (bh, d, n), {"perm": (0, 2, 1)})
+            scores = b.emit("matmul", (qs, ktt), f"{p}.scores", (bh, n, n))
+            probs = b.emit("softmax", (scores,), f"{p}.probs", (bh, n, n), {"axis": -1})
+            ctx = b.emit("matmul", (probs, qkv["v"]), f"{p}.ctx", (bh, n, d))
+            if B == 1:
+                ctxt = b.emit("transpose", (ctx,), f"{p}.ctx.t", (n, heads, d), {"perm": (1, 0, 2)})
+            else:
+                c4 = b.emit("reshape", (ctx,), f"{p}.ctx.b4", (B, heads, n, d),
+                            {"shape": (B, heads, n, d)})
+                ctxt = b.emit("transpose", (c4,), f"{p}.ctx.t", (B, n, heads, d),
+                              {"perm": (0, 2, 1, 3)})
         ctxf = b.emit("reshape", (ctxt,), f"{p}.ctx.f", (rows, H), {"shape": (rows, H)})
         proj = b.linear(ctxf, f"{p}.wo", f"{p}.bo", H, H, f"{p}.o.out")
         x_attn = b.emit("add", (x, proj), f"{p}.resid1", (rows, H))

@@ -91,6 +91,8 @@ def emit_entry(name: str, spec: RunnerSpec) -> str:
     for i, ext in enumerate(spec.extents):
         lines.append(f"    if ((unsigned __int128) ({ext}) > (unsigned __int128) hx_numel(a, {i})) "
                      f"return HEXLIB_DSP_ERR_INVAL_PARAMS;")
+    for cond in spec.checks:
+        lines.append(f"    if (!({cond})) return HEXLIB_DSP_ERR_INVAL_PARAMS;")
     bufs = []
     for i, dt in enumerate(spec.inputs):
         ctype = "unsigned char" if dt in WIRE_RAW else _CTYPE[dt]

@@ -187,6 +187,7 @@ class GpuBackend:
             in_dtypes: Sequence[str] | None = None):
         name, spec = select(kind, attrs, in_dtypes, weight_layout)
         spec.check_requires(attrs)
+        spec.check_rank([a[1] if isinstance(a, tuple) else np.shape(a) for a in arrays])
         if len(arrays) != len(spec.inputs):
             raise GpuError(f"{kind} takes {len(spec.inputs)} inputs, got {len(arrays)}")
         lays = spec.buf_layouts()
@@ -238,9 +239,10 @@ class GpuBackend:
 class _Meta:
     """Shape/dtype stand-in handed to an OpDef's infer."""
 
-    def __init__(self, shape, dtype):
+    def __init__(self, shape, dtype, name="input"):
         self.shape = tuple(shape)
         self.dtype = dtype
+        self.name = name
 
 
 def interpreter_backends(gpu: GpuBackend, kinds=None) -> dict:

@@ -46,6 +46,7 @@ KIND_ID: dict[str, int] = {
     "matmul_epilogue_q4k": 15,
     "transpose_bth": 16,
     "matmul_epilogue_f16wt": 17,
+    "attention": 18,
 }
 
 
@@ -110,6 +111,8 @@ class RunnerSpec:
     requires: tuple[tuple[str, Any], ...] = ()
     layouts: tuple[str, ...] = ()
     extents: tuple[str, ...] = ()   # min element count per buffer (C expressions)
+    checks: tuple[str, ...] = ()    # C conditions on the scalars / buffers, else ERR_INVAL_PARAMS
+    rank: int | None = None         # rank of input 0 the scalar sources assume (None: any)
     weight: tuple[int, str] | None = None   # (input index, dtype) this variant is chosen by
     primary: bool = True            # the reference's own variant when several match
     notes: str = ""
@@ -134,6 +137,13 @@ class RunnerSpec:
 
     def accepts(self, attrs: Mapping[str, Any]) -> bool:
         return all(attrs.get(k) == v for k, v in self.requires)
+
+    def check_rank(self, shapes: Sequence[tuple[int, ...]]) -> None:
+        """The wire pads `ne` to four with ones, so a spec's `dim:`/`rows:`
+        sources silently mean different axes at another rank; refuse it on the
+        host rather than run a correctly-shaped wrong answer."""
+        if self.rank is not None and len(shapes[0]) != self.rank:
+            raise ValueError(f"{self.entry} takes a rank-{self.rank} input 0, got shape {tuple(shapes[0])}")
 
     def check_requires(self, attrs: Mapping[str, Any]) -> None:
         for key, want in self.requires:
@@ -176,17 +186,20 @@ SPECS: dict[str, RunnerSpec] = {
     "transpose": RunnerSpec(
         "transpose", "transpose_th_fp16", ("fp16",), "fp16",
         (_S("dim:0:0", "T"), _S("dim:0:1", "H"), _S("dim:0:2", "D")),
-        requires=(("perm", (1, 0, 2)),), extents=("(uint64_t)T*H*D", "(uint64_t)T*H*D")),
+        requires=(("perm", (1, 0, 2)),), extents=("(uint64_t)T*H*D", "(uint64_t)T*H*D"),
+        rank=3),
     "transpose_hd": RunnerSpec(
         "transpose", "transpose_hd_fp16", ("fp16",), "fp16",
         (_S("dim:0:0", "B"), _S("dim:0:1", "T"), _S("dim:0:2", "D")),
-        requires=(("perm", (0, 2, 1)),), extents=("(uint64_t)B*T*D", "(uint64_t)B*T*D")),
+        requires=(("perm", (0, 2, 1)),), extents=("(uint64_t)B*T*D", "(uint64_t)B*T*D"),
+        rank=3),
     "transpose_bth": RunnerSpec(
         "transpose", "transpose_bth_fp16", ("fp16",), "fp16",
         (_S("dim:0:0", "B"), _S("dim:0:1", "T"), _S("dim:0:2", "H"), _S("dim:0:3", "D")),
         requires=(("perm", (0, 2, 1, 3)),),
         extents=("(uint64_t)B*T*H*D", "(uint64_t)B*T*H*D"),
-        notes="extension: [B,T,H,D] -> [B,H,T,D], the batched transpose_th"),
+        notes="extension: [B,T,H,D] -> [B,H,T,D], the batched transpose_th",
+        rank=4),
     "patchify": RunnerSpec(
         "patchify", "patchify_fp32_batched", ("fp32",), "fp32",
         (_S("dim:0:0", "BC"), _S("dim:0:1", "T"), _S("dim:0:2", "H"), _S("dim:0:3", "W"),
@@ -196,51 +209,71 @@ SPECS: dict[str, RunnerSpec] = {
         extents=("(uint64_t)BC*T*H*W",
                  "(uint64_t)(batch > 0 ? batch : 1)*grid_h*grid_w*(BC/(batch > 0 ? batch : 1))*T*patch*patch"),
         notes="params[4] = batch (0 or 1 = one image, reference blobs zero-fill it); "
-              "the image is [batch*C, T, H, W]"),
+              "the image is [batch*C, T, H, W]",
+        rank=4),
     "matmul": RunnerSpec(
         "matmul", "matmul_fp16", ("fp16", "fp16"), "fp16",
         (_S("dim:0:0", "Bn"), _S("dim:0:1", "M"), _S("dim:0:2", "K"), _S("dim:1:2", "N")),
-        extents=("(uint64_t)Bn*M*K", "(uint64_t)Bn*K*N", "(uint64_t)Bn*M*N")),
+        extents=("(uint64_t)Bn*M*K", "(uint64_t)Bn*K*N", "(uint64_t)Bn*M*N"),
+        rank=3),
     "matmul_epilogue": RunnerSpec(
         "matmul_epilogue", "matmul_epilogue_fp16", ("fp16", "q4_0", "fp32"), "fp16",
         _MM_SCALARS, extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
         weight=(1, "q4_0"),
-        notes="q4_0 weight [K, N], blocks along N (the reference kernel ABI)"),
+        notes="q4_0 weight [K, N], blocks along N (the reference kernel ABI)",
+        rank=2),
     "matmul_epilogue_q4k": RunnerSpec(
         "matmul_epilogue", "matmul_epilogue_q4k_fp16", ("fp16", "q4_0", "fp32"), "fp16",
         _MM_SCALARS,
         layouts=("row_major", "q4_0_kgroup", "row_major", "row_major"),
         extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
         weight=(1, "q4_0"), primary=False,
-        notes="q4_0 weight, logical [K, N] on the wire, stored as W^T [N, K] blocked along K"),
+        notes="q4_0 weight, logical [K, N] on the wire, stored as W^T [N, K] blocked along K",
+        rank=2),
     "matmul_epilogue_f16w": RunnerSpec(
         "matmul_epilogue", "matmul_epilogue_f16w_fp16", ("fp16", "fp16", "fp32"), "fp16",
         _MM_SCALARS, extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
         weight=(1, "fp16"), primary=False,
-        notes="fp16 weight [K, N] row-major"),
+        notes="fp16 weight [K, N] row-major",
+        rank=2),
     "matmul_epilogue_f16wt": RunnerSpec(
         "matmul_epilogue", "matmul_epilogue_f16wt_fp16", ("fp16", "fp16", "fp32"), "fp16",
         _MM_SCALARS,
         layouts=("row_major", "col_major", "row_major", "row_major"),
         extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
         weight=(1, "fp16"), primary=False,
-        notes="fp16 weight, logical [K, N] on the wire, stored as W^T [N, K] (K contiguous)"),
+        notes="fp16 weight, logical [K, N] on the wire, stored as W^T [N, K] (K contiguous)",
+        rank=2),
     "softmax": RunnerSpec(
         "softmax", "softmax_fp16", ("fp16",), "fp16",
         (_S("rows:0:2", "R"), _S("dim:0:2", "C")), requires=(("axis", -1),),
-        extents=("(uint64_t)R*C", "(uint64_t)R*C")),
+        extents=("(uint64_t)R*C", "(uint64_t)R*C"),
+        rank=3),
     "rope_2d": RunnerSpec(
         "rope_2d", "rope_2d_fp16", ("fp16", "fp32", "fp32"), "fp16",
         (_S("dim:0:0", "T"), _S("dim:0:1", "H"), _S("dim:0:2", "D")),
-        extents=("(uint64_t)T*H*D", "(uint64_t)T*D", "(uint64_t)T*D", "(uint64_t)T*H*D")),
+        extents=("(uint64_t)T*H*D", "(uint64_t)T*D", "(uint64_t)T*D", "(uint64_t)T*H*D"),
+        rank=3),
     "layernorm": RunnerSpec(
         "layernorm", "layernorm_fp16", ("fp16", "fp32", "fp32"), "fp16",
         (_S("rows:0:1", "R"), _S("dim:0:1", "C"), _S("attr:eps", "eps", "float")),
-        extents=("(uint64_t)R*C", "C", "C", "(uint64_t)R*C")),
+        extents=("(uint64_t)R*C", "C", "C", "(uint64_t)R*C"),
+        rank=2),
     "rmsnorm": RunnerSpec(
         "rmsnorm", "rmsnorm_fp16", ("fp16", "fp16"), "fp16",
         (_S("rows:0:1", "R"), _S("dim:0:1", "C"), _S("attr:eps", "eps", "float")),
-        extents=("(uint64_t)R*C", "C", "(uint64_t)R*C")),
+        extents=("(uint64_t)R*C", "C", "(uint64_t)R*C"),
+        rank=2),
+    "attention": RunnerSpec(
+        "attention", "attention_fp16", ("fp16", "fp16", "fp16"), "fp16",
+        (_S("dim:0:0", "rows"), _S("dim:0:1", "H"), _S("dim:0:2", "D"),
+         _S("attr:batch", "batch"), _S("attr:scale", "scale", "float")),
+        extents=("(uint64_t)rows*H*D",) * 4,
+        checks=("D == 32 || D == 64", "rows % batch == 0", "(uint64_t)batch * H <= 65535",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
+                "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 7) == 0"),
+        notes="extension: fused softmax(scale q k^T) v over [batch*T, H, D] q/k/v",
+        rank=3),
 }
 
 

@@ -87,6 +87,7 @@ def _spec_for(op, graph: Graph, weight_layout: str | None) -> tuple[str, RunnerS
         layout = "col_major" if op.kind == "matmul_epilogue" and dtypes[1] == "fp16" else None
     name, spec = select(op.kind, dict(op.attrs), dtypes, layout)
     spec.check_requires(dict(op.attrs))
+    spec.check_rank([graph.tensor(n).shape for n in op.inputs])
     return name, spec
 
 

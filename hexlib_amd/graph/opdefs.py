@@ -114,6 +114,17 @@ def _rope_infer(inputs, attrs):
     return ((x.shape, x.dtype),)
 
 
+def _attention_infer(inputs, attrs):
+    q, k, v = inputs
+    if len(q.shape) != 3 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"attention wants q, k, v of one [rows, heads, head_dim] shape, "
+                         f"got {q.shape} {k.shape} {v.shape}")
+    batch = int(attrs.get("batch", 1))
+    if batch < 1 or q.shape[0] % batch:
+        raise ValueError(f"attention: {q.shape[0]} rows do not split into {batch} images")
+    return ((q.shape, q.dtype),)
+
+
 for _kind, _fn in (
     ("add", _add_infer),
     ("scale", _same),
@@ -129,5 +140,6 @@ for _kind, _fn in (
     ("reshape", _reshape_infer),
     ("patchify", _patchify_infer),
     ("rope_2d", _rope_infer),
+    ("attention", _attention_infer),
 ):
     register(OpDef(kind=_kind, infer=_fn))

@@ -9,7 +9,7 @@
  *     dimensions make the call a silent no-op, as in the reference.
  *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
  *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
- *     KIND_ID (1-12) plus appended ids 13-17. Generated from the host's
+ *     KIND_ID (1-12) plus appended ids 13-18. Generated from the host's
  *     RunnerSpec table (hexlib_amd/exec/genentry.py).
  *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
  *     stop/close/hwinfo) that validates a batch blob on the host, resolves
@@ -200,6 +200,16 @@ void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *wt,
 void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
                               const float *bias, hexlib_hf *out,
                               int M, int K, int N, int act);
+/* Fused full attention (KIND 18): out = softmax(scale * q k^T) v for each of
+ * batch images and H heads; q, k, v, out are [rows = batch * T, H, D] fp16
+ * (token-major, the layout rope_2d and the linears produce), D = 32 or 64.
+ * Replaces the reference's scale -> transpose_hd -> matmul -> softmax ->
+ * matmul chain and its transposes (hexlib/models/vit.py:185-193). fp32
+ * scores and online softmax; probabilities rounded to fp16 for the P.V
+ * product; output rounded once. No-op unless rows % batch == 0, q/k/v are
+ * 16-byte aligned and out 8-byte aligned. */
+void attention_fp16(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v,
+                    hexlib_hf *out, int rows, int H, int D, int batch, float scale);
 
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
@@ -218,6 +228,7 @@ int matmul_epilogue_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16w_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q4k_fp16_entry(const hexlib_args *a);
+int attention_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

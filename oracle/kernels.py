@@ -23,6 +23,7 @@ any summation order the GPU picks.
 | matmul_epilogue_fp16 | kernels/matmul_epilogue_fp16/baseline.c:27-97     | _ref (0.01,3e-4) |
 | matmul_epilogue_f16w | hexlib/graph/opdefs/fused.py:44-53 with fp16 w    | reduces to matmul_epilogue_fp16 on dequantized weights |
 | matmul_q4k           | q4_0 blocks along K of W^T, same numerics as q4_0 | reduces to matmul_epilogue_fp16 via a block transpose |
+| attention_fp16       | hexlib/models/vit.py:185-193 chain, fused         | equals the composition of the registry references; uniform / one-hot closed forms |
 """
 from __future__ import annotations
 
@@ -151,3 +152,12 @@ def close_f16(got, want, rel, abs_tol):
     g, w = _f32(got).astype(np.float64), _f32(want).astype(np.float64)
     d = np.abs(g - w)
     return (d <= abs_tol) | (d <= rel * np.maximum(np.abs(g), np.abs(w)))
+
+
+def attention_fp16(q, k, v, batch, scale):
+    """Fused attention over [batch*T, H, D] fp16 q/k/v: float64 inside, one
+    rounding to fp16 (the kernel's contract)."""
+    from oracle.refs import attention
+    (o,) = attention([np.asarray(q, np.float64), np.asarray(k, np.float64), np.asarray(v, np.float64)],
+                     {"batch": batch, "scale": scale})
+    return o.astype(np.float16)

@@ -117,10 +117,29 @@ def rope_2d(arrays, attrs):  # structural.py:240-254
     return ((xf * cosf + rotated * sinf).astype(x.dtype),)
 
 
+def attention(arrays, attrs):
+    """Fused attention: the chain it replaces in the encoder
+    (`hexlib/models/vit.py:185-193`: scale, transpose_hd, matmul, softmax,
+    matmul, with the head transposes around it) computed in float64 with no
+    intermediate storage rounding; q, k, v, out are [batch*T, H, D]."""
+    q, k, v = (np.asarray(a, np.float64) for a in arrays)
+    batch = int(attrs.get("batch", 1))
+    rows, heads, d = q.shape
+    t = rows // batch
+
+    def split(x):  # [B*T, H, D] -> [B, H, T, D]
+        return x.reshape(batch, t, heads, d).transpose(0, 2, 1, 3)
+
+    s = split(q) @ split(k).transpose(0, 1, 3, 2) * float(attrs["scale"])
+    e = np.exp(s - s.max(axis=-1, keepdims=True))
+    o = (e / e.sum(axis=-1, keepdims=True)) @ split(v)
+    return (o.transpose(0, 2, 1, 3).reshape(rows, heads, d).astype(arrays[0].dtype),)
+
+
 REFERENCES = {
     "add": add, "scale": scale, "layernorm": layernorm, "rmsnorm": rmsnorm,
     "gelu_tanh": gelu_tanh, "gelu_erf": gelu_erf, "softmax": softmax,
     "matmul": matmul, "matmul_epilogue": matmul_epilogue, "cast": cast,
     "transpose": transpose, "reshape": reshape, "patchify": patchify,
-    "rope_2d": rope_2d,
+    "rope_2d": rope_2d, "attention": attention,
 }

@@ -1,0 +1,71 @@
+"""Fused attention (KIND 18, `attention_fp16`) on the GPU through the C ABI,
+against the float64 oracle (`oracle.kernels.attention_fp16`): encoder shapes
+(256 and 784 tokens, 12 heads of 64), ragged token counts that leave partial
+query and key tiles, head_dim 32, several images per call, and the closed
+forms. Tolerance: the matmul harness's (rel 1e-2, abs 1e-3,
+`kernels/matmul_fp16/harness.c:145`); the kernel rounds the probabilities to
+fp16 once before the P.V product, as the unfused chain rounds them."""
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+from tests.gpu_util import Dev, h16, report
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev(torch_gpu):
+    return Dev(torch_gpu)
+
+
+def run(dev, q, k, v, B, scale):
+    rows, H, D = q.shape
+    dq, dk, dv = dev.up(q), dev.up(k), dev.up(v)
+    do = dev.empty((rows, H, D), np.float16)
+    dev.lib.attention_fp16(dev.ptr(dq), dev.ptr(dk), dev.ptr(dv), dev.ptr(do), rows, H, D, B, scale)
+    dev.check()
+    return dev.down(do)
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (1, 17, 3, 32), (2, 33, 2, 64),
+                                     (1, 1, 1, 64), (3, 64, 4, 32), (1, 96, 2, 64), (4, 256, 2, 64)])
+def test_attention(dev, B, T, H, D):
+    r = np.random.default_rng(60 + T)
+    q, k, v = (h16(r.standard_normal((B * T, H, D))) for _ in range(3))
+    got = run(dev, q, k, v, B, D ** -0.5)
+    want = K.attention_fp16(q, k, v, B, D ** -0.5)
+    report(f"attention B{B} T{T} H{H} D{D}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+def test_attention_sharp_scores(dev):
+    """Large logits (scale 1, |q.k| up to ~60): the running max must keep
+    exp2 in range; compared with the oracle."""
+    r = np.random.default_rng(70)
+    q, k, v = (h16(r.standard_normal((256, 4, 64)) * 1.0) for _ in range(3))
+    got = run(dev, q, k, v, 1, 1.0)
+    want = K.attention_fp16(q, k, v, 1, 1.0)
+    report("attention sharp", got, want)
+    assert np.isfinite(got.astype(np.float32)).all()
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+def test_attention_uniform_is_mean_of_v(dev):
+    r = np.random.default_rng(71)
+    T, H, D = 100, 3, 64
+    q = h16(np.zeros((T, H, D)))
+    k, v = (h16(r.standard_normal((T, H, D))) for _ in range(2))
+    got = run(dev, q, k, v, 1, 0.125)
+    want = np.broadcast_to(v.astype(np.float64).mean(axis=0), got.shape)
+    assert np.abs(got.astype(np.float64) - want).max() <= 2e-3
+
+
+def test_attention_invalid_is_a_silent_no_op(dev):
+    x = h16(np.ones((64, 2, 48)))
+    dx = dev.up(x)
+    do = dev.empty((64, 2, 48), np.float16)
+    dev.lib.attention_fp16(dev.ptr(dx), dev.ptr(dx), dev.ptr(dx), dev.ptr(do), 64, 2, 48, 1, 0.1)   # D=48
+    dev.lib.attention_fp16(dev.ptr(dx), dev.ptr(dx), dev.ptr(dx), dev.ptr(do), 63, 2, 32, 2, 0.1)   # 63 % 2
+    dev.check()
+    assert (dev.down(do) == np.float16(12345.0)).all()

@@ -52,7 +52,8 @@ def _oracle(cfg, feeds, dense_weights=None):
     return eager.run_stored(g, f)[g.outputs[0]]
 
 
-@pytest.mark.parametrize("cfg", [E.TINY_ENCODER, replace(E.TINY_ENCODER, norm="layernorm")])
+@pytest.mark.parametrize("cfg", [E.TINY_ENCODER, replace(E.TINY_ENCODER, norm="layernorm"),
+                                 replace(E.TINY_ENCODER, attention="fused")])
 def test_tiny_encoder_eager_and_graph(session, cfg):
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=0)
@@ -186,7 +187,7 @@ def test_interpreter_backends_every_kind(session):
         ("add", [f(64, 96), f(64, 96)], {}, [True, True]),
         ("scale", [f(12, 64, 32)], {"factor": 0.125}, [True]),
         ("cast", [f(64, 96)], {"dtype": "fp16"}, [False]),
-        ("softmax", [f(6, 256)], {"axis": -1}, [True]),
+        ("softmax", [f(2, 6, 256)], {"axis": -1}, [True]),
         ("layernorm", [f(16, 768), 1 + 0.02 * f(768), 0.02 * f(768)], {"eps": 1e-6}, [True, False, False]),
         ("rmsnorm", [f(16, 768), 1 + 0.02 * f(768)], {"eps": 1e-6}, [True, True]),
         ("rope_2d", [f(T, 2, cos.shape[1]), cos, sin], {}, [True, False, False]),
@@ -211,3 +212,21 @@ def test_interpreter_backends_every_kind(session):
     (got,) = be["matmul_epilogue"]([a, w, b], {"act": "gelu_tanh"})
     want = K.matmul_epilogue_fp16(a.astype(np.float16), pack_q4_0_nblocked(w), b, 128, 64, 1)
     assert K.close_f16(got, want, 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("image,batch", [(256, 1), (448, 1), (256, 4)])
+def test_fused_attention_encoder_matches_the_reference_graph(session, image, batch):
+    """The plan with one fused attention op per block against the storage-
+    rounding oracle of the REFERENCE graph (unfused attention chain): the
+    whole-encoder bar, <= 2e-2 max abs."""
+    base = E.QWEN35_VISION_FP16 if image == 256 else E.encoder_at(image)
+    cfg_ref = replace(base, batch=batch)
+    g_ref = E.build_vision_encoder(cfg_ref)
+    feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=4)
+    cfg = replace(cfg_ref, attention="fused")
+    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True)
+    assert wb.n_ops == 259 - 12 * 8
+    want = _oracle(cfg_ref, feeds)
+    err = np.abs(out - want).max()
+    print(f"[fused attention {image} b{batch}] max abs vs reference graph {err:.3e}", flush=True)
+    assert err <= 2e-2

@@ -154,3 +154,30 @@ def test_whole_plan_q4_layouts():
     assert "matmul_epilogue_q4k" in b.op_specs
     assert b.placements["blk0.wq"].layout == "q4_0_kgroup"
     assert a.placements["blk0.wq"].nbytes == 64 * 64 // 32 * 18
+
+
+def test_a_spec_refuses_the_wrong_rank():
+    """`ne` is padded to four, so softmax's rows:0:2 / dim:0:2 read a rank-2
+    input as C = 1 -- a correctly-shaped wrong answer. The host refuses it."""
+    from hexlib_amd.exec.runner import SPECS
+    SPECS["softmax"].check_rank([(12, 256, 256)])
+    with pytest.raises(ValueError, match="rank-3"):
+        SPECS["softmax"].check_rank([(6, 256)])
+    with pytest.raises(ValueError, match="rank-2"):
+        SPECS["layernorm"].check_rank([(2, 256, 768)])
+    SPECS["add"].check_rank([(5,)])
+
+
+def test_fused_attention_plan():
+    """attention="fused": one attention op per block replaces the eight ops
+    of the reference chain (3 head transposes, scale, transpose_hd, 2 matmuls,
+    softmax, output transpose -> 9 ops, minus the new one)."""
+    from dataclasses import replace as _replace
+    from hexlib_amd.exec.runner import KIND_ID
+    for cfg in (_replace(E.QWEN35_VISION_FP16, attention="fused"),
+                _replace(E.QWEN35_VISION_FP16, attention="fused", batch=2)):
+        g = E.build_vision_encoder(cfg)
+        wb = WP.build_whole_plan_batch(g, E.synthetic_feeds(g, cfg))
+        assert wb.n_ops == 259 - 12 * 8
+        assert sum(1 for s in wb.op_specs if s == "attention") == 12
+        assert KIND_ID["attention"] == 18

@@ -241,3 +241,24 @@ def test_whole_encoder_blob_dry_runs(sess):
     sess.mmap(0, wb.arena_bytes)
     rc, rsp = sess.invoke(wb.blob, cap=wire.RSP_HDR_SIZE + wire.RESULT_SIZE * wb.n_ops)
     assert rc == OK and rsp.n_ops == wb.n_ops and rsp.ok
+
+
+def _attention_blob(rows, H, D, batch, align_out=0):
+    n = rows * H * D * 2
+    step = (n + 255) // 256 * 256
+    t = [wire.TensorDesc(0, i * step, n, "fp16", "row_major", (rows, H, D, 1)) for i in range(3)]
+    t.append(wire.TensorDesc(0, 3 * step + align_out, n, "fp16", "row_major", (rows, H, D, 1)))
+    op = wire.OpDesc(KIND_ID["attention"], (batch, wire.float_param(D ** -0.5)), (0, 1, 2), (3,))
+    return wire.pack_batch([wire.BufDesc(3, 4 * step + 256)], t, [op]), 4 * step + 256
+
+
+@pytest.mark.parametrize("rows,H,D,batch,align_out,want", [
+    (256, 12, 64, 1, 0, "OK"), (66, 2, 32, 2, 0, "OK"),
+    (256, 12, 48, 1, 0, "ERR_INVAL_PARAMS"),      # head_dim the kernel has no tile for
+    (257, 2, 64, 2, 0, "ERR_INVAL_PARAMS"),       # rows do not split into images
+    (64, 2, 64, 0, 0, "ERR_INVAL_PARAMS"),        # batch 0
+    (64, 2, 64, 1, 2, "ERR_INVAL_PARAMS")])       # misaligned output
+def test_attention_entry_checks(sess, rows, H, D, batch, align_out, want):
+    blob, size = _attention_blob(rows, H, D, batch, align_out)
+    assert sess.mmap(3, size) == OK
+    assert sess.invoke(blob)[0] == wire.STATUS[want]

@@ -290,3 +290,54 @@ def test_batched_patchify_is_per_image_patchify():
     got = K.patchify_fp32(img, p, m, gh, gw, batch=B)
     want = np.concatenate([R.patchify_fp32(img[b * C:(b + 1) * C], p, m, gh, gw) for b in range(B)])
     np.testing.assert_array_equal(got, want)
+
+
+# ---- fused attention (extension) ---------------------------------------------------
+
+def _attn_inputs(B, T, H, D, seed):
+    r = rng(seed)
+    return [r.standard_normal((B * T, H, D)).astype(np.float32) for _ in range(3)]
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 16, 2, 32), (2, 9, 3, 64)])
+def test_attention_is_the_chain_of_registry_references(B, T, H, D):
+    """The fused op equals the reference chain it replaces (vit.py:185-193),
+    composed from the pinned registry references: per image, [T,H,D] ->
+    transpose(1,0,2) -> scale -> matmul with transpose(0,2,1) of k -> softmax
+    -> matmul with v -> transpose(1,0,2)."""
+    from oracle.refs import REFERENCES as RF
+    q, k, v = _attn_inputs(B, T, H, D, 50)
+    scale = D ** -0.5
+    (got,) = RF["attention"]([q, k, v], {"scale": scale, "batch": B})
+    for b in range(B):
+        sl = slice(b * T, (b + 1) * T)
+        qt, kt, vt = (RF["transpose"]([x[sl]], {"perm": (1, 0, 2)})[0] for x in (q, k, v))
+        qs = RF["scale"]([qt], {"factor": scale})[0]
+        ktt = RF["transpose"]([kt], {"perm": (0, 2, 1)})[0]
+        p = RF["softmax"]([RF["matmul"]([qs, ktt], {})[0]], {"axis": -1})[0]
+        ctx = RF["matmul"]([p, vt], {})[0]
+        want = RF["transpose"]([ctx], {"perm": (1, 0, 2)})[0]
+        np.testing.assert_allclose(got[sl], want, rtol=1e-4, atol=1e-5)
+
+
+def test_attention_closed_forms():
+    """q = 0: uniform weights, the output is each head's mean of v over keys.
+    A key whose score dominates: the output is that key's v row."""
+    from oracle.refs import attention
+    _, k, v = _attn_inputs(1, 12, 2, 32, 51)
+    q = np.zeros_like(k)
+    (o,) = attention([q, k, v], {"scale": 0.125, "batch": 1})
+    np.testing.assert_allclose(o, np.broadcast_to(v.mean(axis=0), o.shape), rtol=1e-6, atol=1e-7)
+    q = np.broadcast_to(k[5] * 50.0, k.shape).copy()      # key 5 aligns with every query
+    k2 = k.copy()
+    k2[5] *= 4.0
+    (o,) = attention([q, k2, v], {"scale": 1.0, "batch": 1})
+    np.testing.assert_allclose(o, np.broadcast_to(v[5], o.shape), rtol=1e-5, atol=1e-5)
+
+
+def test_nearmiss_attention_without_scale_fails():
+    from oracle.refs import attention
+    q, k, v = _attn_inputs(1, 16, 2, 32, 52)
+    (good,) = attention([q, k, v], {"scale": 32 ** -0.5, "batch": 1})
+    (bad,) = attention([q, k, v], {"scale": 1.0, "batch": 1})
+    assert not close(bad.astype(np.float16), good.astype(np.float16), 1e-2, 1e-3)
