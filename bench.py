@@ -6,9 +6,10 @@ roofline fractions and the CPU oracle timed beside it.
 A step is one whole-plan replay of the ViT encoder (BASELINE cfg 4: 12
 blocks, hidden 768, 12 heads, MLP 3072, LayerNorm, 2D RoPE, merger) over one
 256x256 image, replayed as ONE captured hipGraph through the session's batch
-invoke. The plan is the product default: each block's attention chain runs as
-one fused attention op (163 launches); the reference graph's unfused plan (259
-launches) is reported as a variant. Inputs and weights are resident in HBM
+invoke. The plan is the product default: per block, one [768, 2304] q/k/v
+linear and one attention op that applies rope_2d itself (115 launches); the
+reference graph's unfused plan (259 launches) is reported as a variant.
+Inputs and weights are resident in HBM
 before timing starts. `value` is images/sec over exactly K replays bracketed
 by device synchronisation.
 
@@ -450,8 +451,8 @@ def main() -> int:
     from hexlib_amd.exec.gpu import GpuPlan, GpuSession
 
     session = GpuSession()
-    cfg = replace(E.QWEN35_VISION_FP16, attention="fused")
-    log("building cfg-4 plan (256x256, batch 1, fused attention)")
+    cfg = replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
+    log("building cfg-4 plan (256x256, batch 1, fused q/k/v + rope + attention)")
     g, feeds, wb = build_plan(cfg)
     plan = GpuPlan(wb, session)
     if args.roofline_only:
@@ -492,7 +493,7 @@ def main() -> int:
     variants = {}
     if not args.no_variants:
         for label, vcfg, steps in (("256_b32", replace(cfg, batch=32), max(5, args.steps // 10)),
-                                   ("448_b1", replace(E.encoder_at(448), attention="fused"),
+                                   ("448_b1", replace(E.encoder_at(448), attention="fused_qkv_rope"),
                                     max(10, args.steps // 2)),
                                    ("256_b1_reference_graph", E.QWEN35_VISION_FP16, max(10, args.steps // 2))):
             log(f"variant {label}")
@@ -515,9 +516,9 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: seeded U[0,1] image, N(0,0.02) fp16 weights, random init",
         "config": {"workload": "vit_encoder_256_b1 (BASELINE cfg 4: 12 blocks, hidden 768, "
-                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; fused attention, "
-                               f"{wb.n_ops} ops as one hipGraph)",
-                   "image": 256, "batch": 1, "tokens": 256, "attention": "fused",
+                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; one q/k/v linear and "
+                               f"one rope+attention op per block, {wb.n_ops} ops as one hipGraph)",
+                   "image": 256, "batch": 1, "tokens": 256, "attention": cfg.attention,
                    "plan_ops": wb.n_ops, "plan_gpu_ns": plan_gpu_ns},
         "roofline": roof,
         "cpu_baseline": cpu,

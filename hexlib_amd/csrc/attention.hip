@@ -13,10 +13,14 @@
 // probabilities are rounded to fp16 for the P.V product, accumulated in fp32;
 // the output is divided by the fp32 sum and rounded to fp16 once.
 //
-// Structure: one 64-lane wave per 32 queries of one (image, head); keys walk in
-// tiles of 32. Both products run on v_mfma_f32_32x32x16_f16 (lane l supplies
-// row l % 32 of A and column l % 32 of B, 8 consecutive k at 8 * (l / 32);
-// result element i of lane l is D[(i/4)*8 + (l/32)*4 + i%4][l % 32]):
+// Structure: a workgroup of WAVES waves owns 32 queries of one (image, head);
+// wave w takes key tiles w, w + WAVES, ... (32 keys each), with the next
+// tile's K and V loads issued before the current tile is computed, and keeps
+// its own running max, sum and output. The waves' partial results are merged
+// through LDS at the end (rescaled by exp2 of the max differences). Both
+// products run on v_mfma_f32_32x32x16_f16 (lane l supplies row l % 32 of A and
+// column l % 32 of B, 8 consecutive k at 8 * (l / 32); result element i of
+// lane l is D[(i/4)*8 + (l/32)*4 + i%4][l % 32]):
 //   S^T = K Q^T   A = K rows (keys), B = Q^T columns (queries): lane l then
 //                 holds 16 scores of ONE query (l % 32), so the row max / sum
 //                 are in-lane plus one exchange with lane l ^ 32.
@@ -25,8 +29,11 @@
 // To make that true the K rows are loaded in a permuted key order: S^T row r
 // holds key kperm(r), chosen so that P's k index 8h + j of chunk c is key
 // 16c + 8h + j; the V^T operand then reads 8 consecutive keys. V^T is formed
-// through LDS ([D][40] halves, 80-byte rows: the 16 rows one ds_read_b128
-// phase touches fall in 16 distinct bank groups).
+// through a wave-private LDS tile ([D][40] halves, 80-byte rows: the 16 rows
+// one ds_read_b128 phase touches fall in 16 distinct bank groups). LDS
+// operations of one wave complete in order, so the wave-private tile needs no
+// barrier; the only workgroup barrier is before the merge, which every wave
+// reaches.
 #include <cmath>
 
 #include "device.h"
@@ -37,28 +44,104 @@ namespace {
 constexpr int QT = 32;          // queries per wave
 constexpr int KT = 32;          // keys per tile
 constexpr int VT_STRIDE = 40;   // halves per LDS row of V^T
+constexpr int WAVES = 4;        // waves sharing one query tile, splitting its keys
 
 __device__ __forceinline__ int kperm(int r) {
     return 16 * (r >> 4) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
 }
 
+template <int D, bool ROPE>
+struct KvTile {
+    f16x8 k[D / 16];                  // this lane's K row chunks (A operand of S^T)
+    f16x8 v[D / 16];                  // this lane's 16-byte pieces of the V tile
+    float c[ROPE ? D / 16 : 1][8];    // rope tables at the K row's token, same d as k
+    float s[ROPE ? D / 16 : 1][8];
+};
+
+// Rotary embedding (split halves) of one row held as D/16 chunks of 8 halves,
+// chunk kk covering d = 16 kk + 8 hl .. +8: chunk kk and kk + D/32 are the two
+// halves of the same 8 pairs. fp32 products and sum rounded separately, then
+// rounded to fp16 -- the rope_2d_fp16 contract (kernels/rope_2d_fp16/baseline.c).
 template <int D>
-__global__ __launch_bounds__(64) void attn_fwd(const f16 *__restrict__ q, const f16 *__restrict__ k,
-                                               const f16 *__restrict__ v, f16 *__restrict__ o,
-                                               int T, int H, float scale_log2e) {
+__device__ __forceinline__ void rope_chunks(f16x8 x[D / 16], const float c[D / 16][8], const float s[D / 16][8]) {
+#pragma clang fp contract(off)
+    constexpr int HC = D / 32;
+#pragma unroll
+    for (int kk = 0; kk < HC; ++kk)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x0 = (float) x[kk][j], x1 = (float) x[kk + HC][j];
+            const float p0 = x0 * c[kk][j], q0 = x1 * s[kk][j];
+            const float p1 = x1 * c[kk + HC][j], q1 = x0 * s[kk + HC][j];
+            x[kk][j] = (f16) f32_rounded(p0 - q0);
+            x[kk + HC][j] = (f16) f32_rounded(p1 + q1);
+        }
+}
+
+template <int D, bool ROPE>
+__device__ __forceinline__ void load_tables(const float *__restrict__ cs, const float *__restrict__ sn,
+                                            long long row, int hl, float c[D / 16][8], float s[D / 16][8]) {
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+        const float *cr = cs + row * D + 16 * kk + 8 * hl;
+        const float *sr = sn + row * D + 16 * kk + 8 * hl;
+        const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cr), c1 = *reinterpret_cast<const f32x4 *>(cr + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4 *>(sr), s1 = *reinterpret_cast<const f32x4 *>(sr + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c[kk][j] = c0[j]; c[kk][j + 4] = c1[j];
+            s[kk][j] = s0[j]; s[kk][j + 4] = s1[j];
+        }
+    }
+}
+
+template <int D, bool ROPE>
+__device__ __forceinline__ void load_tile(const f16 *__restrict__ kb, const f16 *__restrict__ vb,
+                                          const float *__restrict__ cs, const float *__restrict__ sn,
+                                          long long ld, long long row0, int T, int kt, int krow_key,
+                                          int lane, KvTile<D, ROPE> &t) {
+    constexpr int VCH = D / 8;
+    const int hl = lane >> 5;
+    const int key = min(kt + krow_key, T - 1);   // rows past T are masked after the product
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+        t.k[kk] = *reinterpret_cast<const f16x8 *>(kb + key * ld + 16 * kk + 8 * hl);
+    if constexpr (ROPE) load_tables<D, ROPE>(cs, sn, row0 + key, hl, t.c, t.s);
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) {
+        const int e = lane + 64 * i;
+        const int vkey = kt + e / VCH;
+        // keys past T load as zero: their p is 0, and 0 * garbage could be NaN
+        t.v[i] = vkey < T ? *reinterpret_cast<const f16x8 *>(vb + vkey * ld + (e % VCH) * 8) : f16x8{};
+    }
+}
+
+// q, k, v rows are `ld` halves apart (H*D for separate tensors, 3*H*D inside
+// a fused [rows, 3, H, D] projection); out rows are H*D apart. With ROPE, the
+// rotary embedding (tables [rows, D]) is applied to q and k as they are loaded.
+template <int D, int WAVES, bool ROPE>
+__global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q, const f16 *__restrict__ k,
+                                                       const f16 *__restrict__ v, long long ld,
+                                                       f16 *__restrict__ o, const float *__restrict__ cs,
+                                                       const float *__restrict__ sn, int T, int H,
+                                                       float scale_log2e) {
     constexpr int KC = D / 16;   // 16-wide d chunks of q.k
     constexpr int DT = D / 32;   // 32-row tiles of O^T
     constexpr int VCH = D / 8;   // 16-byte chunks per V row
-    __shared__ __attribute__((aligned(16))) f16 vt[D * VT_STRIDE];
+    __shared__ __attribute__((aligned(16))) f16 vt_all[WAVES][D * VT_STRIDE];
+    __shared__ float part_o[WAVES][QT][D + 1];
+    __shared__ float part_m[WAVES][QT], part_l[WAVES][QT];
 
     const int bh = blockIdx.y;
     const int b = bh / H, h = bh % H;
-    const long long ld = (long long) H * D;   // token stride
-    const long long base = (long long) b * T * ld + (long long) h * D;
-    const f16 *qb = q + base, *kb = k + base, *vb = v + base;
-    f16 *ob = o + base;
-    const int lane = threadIdx.x, hl = lane >> 5, c32 = lane & 31;
+    const long long ldo = (long long) H * D;   // output token stride
+    const long long row0 = (long long) b * T;   // first row of this image
+    const f16 *qb = q + row0 * ld + (long long) h * D, *kb = k + row0 * ld + (long long) h * D,
+              *vb = v + row0 * ld + (long long) h * D;
+    f16 *ob = o + row0 * ldo + (long long) h * D;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
     const int q0 = blockIdx.x * QT;
+    f16 *vt = vt_all[wave];
 
     // B operand of S^T: query column c32, d = 16 kk + 8 hl .. +8
     f16x8 qf[KC];
@@ -67,38 +150,39 @@ __global__ __launch_bounds__(64) void attn_fwd(const f16 *__restrict__ q, const 
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk)
             qf[kk] = *reinterpret_cast<const f16x8 *>(qb + qi * ld + 16 * kk + 8 * hl);
+        if constexpr (ROPE) {
+            float c[KC][8], sv[KC][8];
+            load_tables<D, ROPE>(cs, sn, row0 + qi, hl, c, sv);
+            rope_chunks<D>(qf, c, sv);
+        }
     }
-    const int krow_key = kperm(c32);   // key (within the tile) this lane's K row holds
+    const int krow_key = kperm(c32);   // key (within a tile) this lane's K row holds
 
     f32x16 oacc[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
     float m = -INFINITY, l = 0.f;
 
-    for (int kt = 0; kt < T; kt += KT) {
-        // K operand (A of S^T): row c32 = key kt + kperm(c32), d = 16 kk + 8 hl
-        f16x8 kf[KC];
-        {
-            const int key = min(kt + krow_key, T - 1);   // rows past T are masked below
+    KvTile<D, ROPE> cur, nxt;
+    int kt = wave * KT;
+    if (kt < T) load_tile<D, ROPE>(kb, vb, cs, sn, ld, row0, T, kt, krow_key, lane, cur);
+    for (; kt < T; kt += WAVES * KT) {
+        const int kn = kt + WAVES * KT;
+        if (kn < T) load_tile<D, ROPE>(kb, vb, cs, sn, ld, row0, T, kn, krow_key, lane, nxt);
+        if constexpr (ROPE) rope_chunks<D>(cur.k, cur.c, cur.s);
+
+        // V tile -> wave-private LDS as V^T[d][key]
 #pragma unroll
-            for (int kk = 0; kk < KC; ++kk)
-                kf[kk] = *reinterpret_cast<const f16x8 *>(kb + key * ld + 16 * kk + 8 * hl);
-        }
-        // V tile -> LDS as V^T[d][key]; keys past T are zero (their p is 0,
-        // and 0 * garbage could be NaN)
-#pragma unroll
-        for (int t = 0; t < KT * VCH / 64; ++t) {
-            const int e = lane + 64 * t;
+        for (int i = 0; i < D / 16; ++i) {
+            const int e = lane + 64 * i;
             const int vk = e / VCH, d0 = (e % VCH) * 8;
-            const int key = kt + vk;
-            const f16x8 vv = key < T ? *reinterpret_cast<const f16x8 *>(vb + key * ld + d0) : f16x8{};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vt[(d0 + j) * VT_STRIDE + vk] = vv[j];
+            for (int j = 0; j < 8; ++j) vt[(d0 + j) * VT_STRIDE + vk] = cur.v[i][j];
         }
 
         f32x16 s = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < KC; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], s, 0, 0, 0);
+        for (int kk = 0; kk < KC; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.k[kk], qf[kk], s, 0, 0, 0);
 
         // element i of this lane is key kt + 16 (i / 8) + 8 hl + i % 8
         float tmax = -INFINITY;
@@ -109,7 +193,7 @@ __global__ __launch_bounds__(64) void attn_fwd(const f16 *__restrict__ q, const 
             tmax = fmaxf(tmax, s[i]);
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m, tmax);     // finite: key kt < T is always valid
+        const float m_new = fmaxf(m, tmax);     // finite: key kt < T is valid
         const float alpha = exp2f(m - m_new);
         f16x8 pb[2];
         float psum = 0.f;
@@ -126,7 +210,6 @@ __global__ __launch_bounds__(64) void attn_fwd(const f16 *__restrict__ q, const 
 #pragma unroll
             for (int i = 0; i < 16; ++i) oacc[t][i] *= alpha;
 
-        __syncthreads();   // V^T tile written
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -134,40 +217,79 @@ __global__ __launch_bounds__(64) void attn_fwd(const f16 *__restrict__ q, const 
                 const f16x8 va = *reinterpret_cast<const f16x8 *>(vt + (t * 32 + c32) * VT_STRIDE + 16 * c + 8 * hl);
                 oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], oacc[t], 0, 0, 0);
             }
-        __syncthreads();   // V^T tile consumed before the next one is written
+        cur = nxt;
     }
 
+    // merge the waves: each publishes (m, l, O) for its 32 queries
     l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
-    const int qi = q0 + c32;
-    if (qi >= T) return;
-    // oacc[t][i] = O^T[d = 32 t + (i/4)*8 + 4 hl + i%4][query qi]
+    if (hl == 0) {
+        part_m[wave][c32] = m;
+        part_l[wave][c32] = l;
+    }
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            f16x4 out;
+        for (int i = 0; i < 16; ++i)
+            part_o[wave][c32][32 * t + (i >> 2) * 8 + 4 * hl + (i & 3)] = oacc[t][i];
+    __syncthreads();
+
+    // 32 queries x D outputs, 8 consecutive d per thread
+    for (int e = threadIdx.x; e < QT * (D / 8); e += 64 * WAVES) {
+        const int qq = e / (D / 8), d0 = (e % (D / 8)) * 8;
+        const int qi = q0 + qq;
+        if (qi >= T) continue;
+        float mx = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out[e] = (f16) (oacc[t][4 * g + e] * inv);
-            *reinterpret_cast<f16x4 *>(ob + qi * ld + 32 * t + 8 * g + 4 * hl) = out;
+        for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, part_m[w][qq]);
+        float wsum = 0.f, acc[8] = {};
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float a = exp2f(part_m[w][qq] - mx);   // 0 for a wave that saw no key
+            wsum += a * part_l[w][qq];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += a * part_o[w][qq][d0 + j];
         }
+        const float inv = 1.0f / wsum;
+        f16x8 out;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = (f16) (acc[j] * inv);
+        *reinterpret_cast<f16x8 *>(ob + qi * ldo + d0) = out;
+    }
 }
 
-}  // namespace
-
-extern "C" void attention_fp16(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v,
-                               hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
-    if (!q || !k || !v || !out || rows <= 0 || H <= 0 || batch <= 0 || rows % batch) return;
-    if (D != 32 && D != 64) return;
-    if (!hx::aligned(q, 16) || !hx::aligned(k, 16) || !hx::aligned(v, 16) || !hx::aligned(out, 8)) return;
+template <bool ROPE>
+void launch(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v, long long ld, hexlib_hf *out,
+            const float *cs, const float *sn, int rows, int H, int D, int batch, float scale) {
     const int T = rows / batch;
-    if ((long long) batch * H > 65535) return;
     const dim3 grid((unsigned) ((T + QT - 1) / QT), (unsigned) (batch * H));
     const float sl2e = scale * 1.4426950408889634f;
     const auto *Q = reinterpret_cast<const f16 *>(q);
     const auto *K = reinterpret_cast<const f16 *>(k);
     const auto *V = reinterpret_cast<const f16 *>(v);
     auto *O = reinterpret_cast<f16 *>(out);
-    if (D == 64) HX_LAUNCH(attn_fwd<64>, grid, dim3(64), 0, Q, K, V, O, T, H, sl2e);
-    else HX_LAUNCH(attn_fwd<32>, grid, dim3(64), 0, Q, K, V, O, T, H, sl2e);
+    if (D == 64) HX_LAUNCH((attn_fwd<64, WAVES, ROPE>), grid, dim3(64 * WAVES), 0, Q, K, V, ld, O, cs, sn, T, H, sl2e);
+    else HX_LAUNCH((attn_fwd<32, WAVES, ROPE>), grid, dim3(64 * WAVES), 0, Q, K, V, ld, O, cs, sn, T, H, sl2e);
+}
+
+bool dims_ok(int rows, int H, int D, int batch) {
+    return rows > 0 && H > 0 && batch > 0 && rows % batch == 0 && (D == 32 || D == 64) &&
+           (long long) batch * H <= 65535;
+}
+
+}  // namespace
+
+extern "C" void attention_fp16(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v,
+                               hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
+    if (!q || !k || !v || !out || !dims_ok(rows, H, D, batch)) return;
+    if (!hx::aligned(q, 16) || !hx::aligned(k, 16) || !hx::aligned(v, 16) || !hx::aligned(out, 16)) return;
+    launch<false>(q, k, v, (long long) H * D, out, nullptr, nullptr, rows, H, D, batch, scale);
+}
+
+extern "C" void attention_qkv_rope_fp16(const hexlib_hf *qkv, const float *costab, const float *sintab,
+                                        hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
+    if (!qkv || !costab || !sintab || !out || !dims_ok(rows, H, D, batch)) return;
+    if (!hx::aligned(qkv, 16) || !hx::aligned(out, 16) || !hx::aligned(costab, 16) || !hx::aligned(sintab, 16))
+        return;
+    const long long hd = (long long) H * D;
+    launch<true>(qkv, qkv + hd, qkv + 2 * hd, 3 * hd, out, costab, sintab, rows, H, D, batch, scale);
 }

@@ -14,6 +14,10 @@ Build extensions (not in the reference, each optional and off by default):
   runs over batch * heads, the per-token tables are replicated per image.
 * `norm="rmsnorm"`: RMSNorm blocks with an fp16 gain and no bias, matching the
   reference's `rmsnorm_fp16` kernel contract.
+* `attention="fused"`: each block's attention chain (head transposes, scale,
+  transpose_hd, two matmuls, softmax) as one `attention` op; `"fused_qkv_rope"`
+  additionally computes q, k, v with one [H, 3H] linear and applies rope_2d
+  inside the attention op (`fuse_qkv_feeds` rewrites reference feeds for it).
 
 Host-side tables (RoPE cos/sin, bilinear pos_embed) restate the reference
 loader (`hexlib/models/loader.py:30-146`).
@@ -21,7 +25,7 @@ loader (`hexlib/models/loader.py:30-146`).
 from __future__ import annotations
 
 from dataclasses import dataclass, fields, replace
-from typing import Any, Callable, get_type_hints
+from typing import Mapping, Any, Callable, get_type_hints
 
 import numpy as np
 
@@ -49,7 +53,10 @@ class VitConfig:
     weight_dtype: str = "fp32"
     norm: str = "layernorm"
     batch: int = 1
-    attention: str = "unfused"   # "fused": one attention op per block (KIND 18)
+    # "unfused": the reference graph; "fused": one attention op per block
+    # (KIND 18); "fused_qkv_rope": one q/k/v linear and one attention op that
+    # applies rope_2d itself (KIND 19)
+    attention: str = "unfused"
 
     @property
     def grid(self) -> int:
@@ -112,7 +119,7 @@ class ConfigError(ValueError):
 
 
 def config_problems(cfg: VitConfig) -> list[str]:
-    """Reference `vit.py:248-283`, plus the two extension fields."""
+    """Reference `vit.py:248-283`, plus the extension fields."""
     out: list[str] = []
     hints = get_type_hints(VitConfig)
     for f in fields(VitConfig):
@@ -130,6 +137,8 @@ def config_problems(cfg: VitConfig) -> list[str]:
         out.append(f"head_dim {cfg.head_dim} must be even for 2D RoPE")
     if cfg.norm not in ("layernorm", "rmsnorm"):
         out.append(f"norm {cfg.norm!r} must be 'layernorm' or 'rmsnorm'")
+    if cfg.attention not in ("unfused", "fused", "fused_qkv_rope"):
+        out.append(f"attention {cfg.attention!r} must be 'unfused', 'fused' or 'fused_qkv_rope'")
     return out
 
 
@@ -204,7 +213,7 @@ def build_vision_encoder(cfg: VitConfig) -> Graph:
         p = f"blk{layer}"
         a = b.norm(x, f"{p}.ln1", f"{p}.ln1.out")
         qkv = {}
-        for which in ("q", "k", "v"):
+        for which in (() if cfg.attention == "fused_qkv_rope" else ("q", "k", "v")):
             proj = b.linear(a, f"{p}.w{which}", f"{p}.b{which}", H, H, f"{p}.{which}.out")
             t = b.emit("reshape", (proj,), f"{p}.{which}.h", (rows, heads, d),
                        {"shape": (rows, heads, d)})
@@ -223,7 +232,14 @@ def build_vision_encoder(cfg: VitConfig) -> Graph:
                             {"perm": (0, 2, 1, 3)})
                 qkv[which] = b.emit("reshape", (t4,), f"{p}.{which}.t", (B * heads, n, d),
                                     {"shape": (B * heads, n, d)})
-        if cfg.attention == "fused":
+        if cfg.attention == "fused_qkv_rope":
+            # one [H, 3H] linear for q, k, v; rope_2d and attention in one op
+            fused = b.linear(a, f"{p}.wqkv", f"{p}.bqkv", H, 3 * H, f"{p}.qkv.out")
+            qkv4 = b.emit("reshape", (fused,), f"{p}.qkv.h", (rows, 3, heads, d),
+                          {"shape": (rows, 3, heads, d)})
+            ctxt = b.emit("attention", (qkv4, cos, sin), f"{p}.ctx.t", (rows, heads, d),
+                          {"scale": float(d) ** -0.5, "batch": B})
+        elif cfg.attention == "fused":
             # one op for the chain below; [rows, heads, d] in and out
             ctxt = b.emit("attention", (qkv["q"], qkv["k"], qkv["v"]), f"{p}.ctx.t", (rows, heads, d),
                           {"scale": float(d) ** -0.5, "batch": B})
@@ -371,6 +387,19 @@ def _check_feeds(graph: Graph, feeds: dict[str, Any]) -> None:
         want = graph.tensor(name).shape
         if tuple(np.shape(value)) != want:
             raise ValueError(f"feed {name!r} is {np.shape(value)}, graph declares {want}")
+
+
+def fuse_qkv_feeds(feeds: Mapping[str, np.ndarray], cfg: VitConfig) -> dict[str, np.ndarray]:
+    """Feeds of the reference graph (separate q/k/v linears) rewritten for
+    attention="fused_qkv_rope": per block, w{q,k,v} [H, H] side by side as
+    wqkv [H, 3H] and b{q,k,v} as bqkv [3H] -- the same values, so both graphs
+    compute the same function."""
+    out = dict(feeds)
+    for layer in range(cfg.depth):
+        p = f"blk{layer}"
+        out[f"{p}.wqkv"] = np.concatenate([out.pop(f"{p}.w{w}") for w in "qkv"], axis=1)
+        out[f"{p}.bqkv"] = np.concatenate([out.pop(f"{p}.b{w}") for w in "qkv"])
+    return out
 
 
 def synthetic_feeds(graph: Graph, cfg: VitConfig, seed: int = 0) -> dict[str, np.ndarray]:

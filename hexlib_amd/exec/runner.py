@@ -47,6 +47,7 @@ KIND_ID: dict[str, int] = {
     "transpose_bth": 16,
     "matmul_epilogue_f16wt": 17,
     "attention": 18,
+    "attention_qkv_rope": 19,
 }
 
 
@@ -271,9 +272,20 @@ SPECS: dict[str, RunnerSpec] = {
         extents=("(uint64_t)rows*H*D",) * 4,
         checks=("D == 32 || D == 64", "rows % batch == 0", "(uint64_t)batch * H <= 65535",
                 "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
-                "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 7) == 0"),
-        notes="extension: fused softmax(scale q k^T) v over [batch*T, H, D] q/k/v",
-        rank=3),
+                "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 15) == 0"),
+        weight=(1, "fp16"), rank=3,
+        notes="extension: fused softmax(scale q k^T) v over [batch*T, H, D] q/k/v"),
+    "attention_qkv_rope": RunnerSpec(
+        "attention", "attention_qkv_rope_fp16", ("fp16", "fp32", "fp32"), "fp16",
+        (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),
+         _S("attr:batch", "batch"), _S("attr:scale", "scale", "float")),
+        extents=("(uint64_t)rows*3*H*D", "(uint64_t)rows*D", "(uint64_t)rows*D", "(uint64_t)rows*H*D"),
+        checks=("a->ne[0][1] == 3", "D == 32 || D == 64", "rows % batch == 0",
+                "(uint64_t)batch * H <= 65535",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
+                "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 15) == 0"),
+        weight=(1, "fp32"), rank=4, primary=False,
+        notes="extension: attention over a fused [rows, 3, H, D] QKV projection, rope_2d on q and k"),
 }
 
 

@@ -115,6 +115,18 @@ def _rope_infer(inputs, attrs):
 
 
 def _attention_infer(inputs, attrs):
+    """(q, k, v) each [rows, heads, head_dim]; or (qkv [rows, 3, heads,
+    head_dim], cos, sin [rows, head_dim]) with the rotary embedding applied to
+    q and k first. Output [rows, heads, head_dim]."""
+    if len(inputs[0].shape) == 4:
+        qkv, cos, sin = inputs
+        rows, three, heads, d = qkv.shape
+        if three != 3 or cos.shape != (rows, d) or sin.shape != (rows, d) or d % 2:
+            raise ValueError(f"attention over fused qkv {qkv.shape} with tables {cos.shape}/{sin.shape}")
+        batch = int(attrs.get("batch", 1))
+        if batch < 1 or rows % batch:
+            raise ValueError(f"attention: {rows} rows do not split into {batch} images")
+        return (((rows, heads, d), qkv.dtype),)
     q, k, v = inputs
     if len(q.shape) != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError(f"attention wants q, k, v of one [rows, heads, head_dim] shape, "

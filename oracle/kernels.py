@@ -24,6 +24,7 @@ any summation order the GPU picks.
 | matmul_epilogue_f16w | hexlib/graph/opdefs/fused.py:44-53 with fp16 w    | reduces to matmul_epilogue_fp16 on dequantized weights |
 | matmul_q4k           | q4_0 blocks along K of W^T, same numerics as q4_0 | reduces to matmul_epilogue_fp16 via a block transpose |
 | attention_fp16       | hexlib/models/vit.py:185-193 chain, fused         | equals the composition of the registry references; uniform / one-hot closed forms |
+| attention_qkv_rope_fp16 | rope_2d_fp16 on q, k, then attention_fp16      | composition of the two pinned functions above |
 """
 from __future__ import annotations
 
@@ -161,3 +162,12 @@ def attention_fp16(q, k, v, batch, scale):
     (o,) = attention([np.asarray(q, np.float64), np.asarray(k, np.float64), np.asarray(v, np.float64)],
                      {"batch": batch, "scale": scale})
     return o.astype(np.float16)
+
+
+def attention_qkv_rope_fp16(qkv, cos, sin, batch, scale):
+    """The fused-projection form: rope_2d_fp16 (with its fp16 rounding) on q
+    and k, then attention_fp16."""
+    qkv = np.asarray(qkv, np.float16)
+    q = rope_2d_fp16(np.ascontiguousarray(qkv[:, 0]), cos, sin)
+    k = rope_2d_fp16(np.ascontiguousarray(qkv[:, 1]), cos, sin)
+    return attention_fp16(q, k, np.ascontiguousarray(qkv[:, 2]), batch, scale)

@@ -121,7 +121,14 @@ def attention(arrays, attrs):
     """Fused attention: the chain it replaces in the encoder
     (`hexlib/models/vit.py:185-193`: scale, transpose_hd, matmul, softmax,
     matmul, with the head transposes around it) computed in float64 with no
-    intermediate storage rounding; q, k, v, out are [batch*T, H, D]."""
+    intermediate storage rounding; q, k, v, out are [batch*T, H, D]. The fused-
+    projection form takes (qkv [batch*T, 3, H, D], cos, sin) and applies the
+    rope_2d reference (float32, structural.py:240-254) to q and k first."""
+    if np.ndim(arrays[0]) == 4:   # (qkv [rows, 3, H, D], cos, sin): rope_2d on q and k first
+        qkv, cos, sin = arrays
+        (qr,) = rope_2d((qkv[:, 0], cos, sin), {})
+        (kr,) = rope_2d((qkv[:, 1], cos, sin), {})
+        arrays = (qr, kr, qkv[:, 2])
     q, k, v = (np.asarray(a, np.float64) for a in arrays)
     batch = int(attrs.get("batch", 1))
     rows, heads, d = q.shape

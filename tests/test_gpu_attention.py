@@ -69,3 +69,31 @@ def test_attention_invalid_is_a_silent_no_op(dev):
     dev.lib.attention_fp16(dev.ptr(dx), dev.ptr(dx), dev.ptr(dx), dev.ptr(do), 63, 2, 32, 2, 0.1)   # 63 % 2
     dev.check()
     assert (dev.down(do) == np.float16(12345.0)).all()
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (2, 33, 2, 64), (3, 17, 2, 32)])
+def test_attention_qkv_rope(dev, B, T, H, D):
+    """KIND 19: q, k, v side by side in one [rows, 3, H, D] projection, rope_2d
+    on q and k inside the kernel. Oracle: rope_2d_fp16 (pinned bit-exact
+    against the reference baseline) then attention."""
+    from hexlib_amd import encoder as E
+    from dataclasses import replace
+    r = np.random.default_rng(80 + T)
+    rows = B * T
+    qkv = h16(r.standard_normal((rows, 3, H, D)))
+    grid = int(round(np.sqrt(T)))
+    if grid * grid == T:
+        cfg = replace(E.QWEN35_VISION_FP16, image_size=16 * grid, hidden_size=H * D, num_heads=H, batch=B)
+        cos, sin = E.rope_tables(cfg)
+    else:
+        ang = r.random((rows, D // 2)) * 6.0
+        cos = np.concatenate([np.cos(ang)] * 2, axis=1).astype(np.float32)
+        sin = np.concatenate([np.sin(ang)] * 2, axis=1).astype(np.float32)
+    dqkv, dc, ds = dev.up(qkv), dev.up(cos), dev.up(sin)
+    do = dev.empty((rows, H, D), np.float16)
+    dev.lib.attention_qkv_rope_fp16(dev.ptr(dqkv), dev.ptr(dc), dev.ptr(ds), dev.ptr(do), rows, H, D, B, D ** -0.5)
+    dev.check()
+    got = dev.down(do)
+    want = K.attention_qkv_rope_fp16(qkv, cos, sin, B, D ** -0.5)
+    report(f"attention_qkv_rope B{B} T{T} H{H} D{D}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()

@@ -53,7 +53,8 @@ def _oracle(cfg, feeds, dense_weights=None):
 
 
 @pytest.mark.parametrize("cfg", [E.TINY_ENCODER, replace(E.TINY_ENCODER, norm="layernorm"),
-                                 replace(E.TINY_ENCODER, attention="fused")])
+                                 replace(E.TINY_ENCODER, attention="fused"),
+                                 replace(E.TINY_ENCODER, attention="fused_qkv_rope")])
 def test_tiny_encoder_eager_and_graph(session, cfg):
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=0)
@@ -214,8 +215,10 @@ def test_interpreter_backends_every_kind(session):
     assert K.close_f16(got, want, 0.01, 3e-4).all()
 
 
-@pytest.mark.parametrize("image,batch", [(256, 1), (448, 1), (256, 4)])
-def test_fused_attention_encoder_matches_the_reference_graph(session, image, batch):
+@pytest.mark.parametrize("image,batch,mode", [(256, 1, "fused"), (448, 1, "fused"), (256, 4, "fused"),
+                                              (256, 1, "fused_qkv_rope"), (448, 1, "fused_qkv_rope"),
+                                              (256, 4, "fused_qkv_rope")])
+def test_fused_attention_encoder_matches_the_reference_graph(session, image, batch, mode):
     """The plan with one fused attention op per block against the storage-
     rounding oracle of the REFERENCE graph (unfused attention chain): the
     whole-encoder bar, <= 2e-2 max abs."""
@@ -223,10 +226,11 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     cfg_ref = replace(base, batch=batch)
     g_ref = E.build_vision_encoder(cfg_ref)
     feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=4)
-    cfg = replace(cfg_ref, attention="fused")
-    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True)
-    assert wb.n_ops == 259 - 12 * 8
+    cfg = replace(cfg_ref, attention=mode)
+    fused_feeds = E.fuse_qkv_feeds(feeds, cfg) if mode == "fused_qkv_rope" else feeds
+    (out,), wb = _run_plan(session, cfg, fused_feeds, graph_mode=True)
+    assert wb.n_ops == 259 - 12 * (8 if mode == "fused" else 12)
     want = _oracle(cfg_ref, feeds)
     err = np.abs(out - want).max()
-    print(f"[fused attention {image} b{batch}] max abs vs reference graph {err:.3e}", flush=True)
+    print(f"[{mode} {image} b{batch}] max abs vs reference graph {err:.3e}", flush=True)
     assert err <= 2e-2

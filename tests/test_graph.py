@@ -181,3 +181,25 @@ def test_fused_attention_plan():
         assert wb.n_ops == 259 - 12 * 8
         assert sum(1 for s in wb.op_specs if s == "attention") == 12
         assert KIND_ID["attention"] == 18
+    for cfg in (_replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope"),
+                _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope", batch=2)):
+        g = E.build_vision_encoder(cfg)
+        wb = WP.build_whole_plan_batch(g, E.synthetic_feeds(g, cfg))
+        assert wb.n_ops == 259 - 12 * 12       # and two fewer linears, no rope ops
+        assert sum(1 for s in wb.op_specs if s == "attention_qkv_rope") == 12
+        assert not any(s == "rope_2d" for s in wb.op_specs)
+        assert KIND_ID["attention_qkv_rope"] == 19
+
+
+def test_fused_qkv_feeds_compute_the_reference_function():
+    """fuse_qkv_feeds only rearranges values: on the oracle, the fused-QKV
+    graph gives the reference graph's output."""
+    from dataclasses import replace as _replace
+    from oracle import eager
+    cfg = E.TINY_ENCODER
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg, seed=3)
+    gq = E.build_vision_encoder(_replace(cfg, attention="fused_qkv_rope"))
+    want = eager.run_fp32(fuse(g), feeds)[g.outputs[0]]
+    got = eager.run_fp32(fuse(gq), E.fuse_qkv_feeds(feeds, cfg))[gq.outputs[0]]
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)

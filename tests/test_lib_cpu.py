@@ -257,8 +257,24 @@ def _attention_blob(rows, H, D, batch, align_out=0):
     (256, 12, 48, 1, 0, "ERR_INVAL_PARAMS"),      # head_dim the kernel has no tile for
     (257, 2, 64, 2, 0, "ERR_INVAL_PARAMS"),       # rows do not split into images
     (64, 2, 64, 0, 0, "ERR_INVAL_PARAMS"),        # batch 0
-    (64, 2, 64, 1, 2, "ERR_INVAL_PARAMS")])       # misaligned output
+    (64, 2, 64, 1, 2, "ERR_INVAL_PARAMS"),        # misaligned output
+    (64, 2, 64, 1, 8, "ERR_INVAL_PARAMS")])
 def test_attention_entry_checks(sess, rows, H, D, batch, align_out, want):
     blob, size = _attention_blob(rows, H, D, batch, align_out)
     assert sess.mmap(3, size) == OK
+    assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+@pytest.mark.parametrize("three,D,want", [(3, 64, "OK"), (2, 64, "ERR_INVAL_PARAMS"), (3, 40, "ERR_INVAL_PARAMS")])
+def test_attention_qkv_rope_entry_checks(sess, three, D, want):
+    rows, H = 64, 2
+    sizes = [rows * three * H * D * 2, rows * D * 4, rows * D * 4, rows * H * D * 2]
+    offs = np.cumsum([0] + [(x + 255) // 256 * 256 for x in sizes])
+    t = [wire.TensorDesc(0, int(offs[0]), sizes[0], "fp16", "row_major", (rows, three, H, D)),
+         wire.TensorDesc(0, int(offs[1]), sizes[1], "fp32", "row_major", (rows, D, 1, 1)),
+         wire.TensorDesc(0, int(offs[2]), sizes[2], "fp32", "row_major", (rows, D, 1, 1)),
+         wire.TensorDesc(0, int(offs[3]), sizes[3], "fp16", "row_major", (rows, H, D, 1))]
+    op = wire.OpDesc(KIND_ID["attention_qkv_rope"], (1, wire.float_param(0.125)), (0, 1, 2), (3,))
+    blob = wire.pack_batch([wire.BufDesc(3, int(offs[4]))], t, [op])
+    assert sess.mmap(3, int(offs[4])) == OK
     assert sess.invoke(blob)[0] == wire.STATUS[want]
