@@ -6,7 +6,9 @@
 //
 // Layout: q, k, v and out are [rows = batch * T, H, D] fp16, the layout rope_2d
 // and the linears produce (token-major, heads interleaved), so no transpose is
-// needed on either side.
+// needed on either side. attention_qk_v_fp16 takes q and k from a
+// [rows, 2, H, D] tensor (rope_2d_qk_fp16's output) and v from the fused
+// [rows, 3, H, D] projection, by row stride.
 //
 // Numerics: q.k in fp32 (MFMA accumulate), scaled in fp32; a running max and
 // sum per query (online softmax, exp2 of log2e-scaled scores); the unnormalised
@@ -50,81 +52,37 @@ __device__ __forceinline__ int kperm(int r) {
     return 16 * (r >> 4) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
 }
 
-template <int D, bool ROPE>
+template <int D>
 struct KvTile {
-    f16x8 k[D / 16];                  // this lane's K row chunks (A operand of S^T)
-    f16x8 v[D / 16];                  // this lane's 16-byte pieces of the V tile
-    float c[ROPE ? D / 16 : 1][8];    // rope tables at the K row's token, same d as k
-    float s[ROPE ? D / 16 : 1][8];
+    f16x8 k[D / 16];       // this lane's K row chunks (A operand of S^T)
+    f16x8 v[D / 16];       // this lane's 16-byte pieces of the V tile
 };
 
-// Rotary embedding (split halves) of one row held as D/16 chunks of 8 halves,
-// chunk kk covering d = 16 kk + 8 hl .. +8: chunk kk and kk + D/32 are the two
-// halves of the same 8 pairs. fp32 products and sum rounded separately, then
-// rounded to fp16 -- the rope_2d_fp16 contract (kernels/rope_2d_fp16/baseline.c).
 template <int D>
-__device__ __forceinline__ void rope_chunks(f16x8 x[D / 16], const float c[D / 16][8], const float s[D / 16][8]) {
-#pragma clang fp contract(off)
-    constexpr int HC = D / 32;
-#pragma unroll
-    for (int kk = 0; kk < HC; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float x0 = (float) x[kk][j], x1 = (float) x[kk + HC][j];
-            const float p0 = x0 * c[kk][j], q0 = x1 * s[kk][j];
-            const float p1 = x1 * c[kk + HC][j], q1 = x0 * s[kk + HC][j];
-            x[kk][j] = (f16) f32_rounded(p0 - q0);
-            x[kk + HC][j] = (f16) f32_rounded(p1 + q1);
-        }
-}
-
-template <int D, bool ROPE>
-__device__ __forceinline__ void load_tables(const float *__restrict__ cs, const float *__restrict__ sn,
-                                            long long row, int hl, float c[D / 16][8], float s[D / 16][8]) {
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-        const float *cr = cs + row * D + 16 * kk + 8 * hl;
-        const float *sr = sn + row * D + 16 * kk + 8 * hl;
-        const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cr), c1 = *reinterpret_cast<const f32x4 *>(cr + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4 *>(sr), s1 = *reinterpret_cast<const f32x4 *>(sr + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            c[kk][j] = c0[j]; c[kk][j + 4] = c1[j];
-            s[kk][j] = s0[j]; s[kk][j + 4] = s1[j];
-        }
-    }
-}
-
-template <int D, bool ROPE>
-__device__ __forceinline__ void load_tile(const f16 *__restrict__ kb, const f16 *__restrict__ vb,
-                                          const float *__restrict__ cs, const float *__restrict__ sn,
-                                          long long ld, long long row0, int T, int kt, int krow_key,
-                                          int lane, KvTile<D, ROPE> &t) {
+__device__ __forceinline__ void load_tile(const f16 *__restrict__ kb, long long ldk, const f16 *__restrict__ vb,
+                                          long long ldv, int T, int kt, int krow_key, int lane, KvTile<D> &t) {
     constexpr int VCH = D / 8;
     const int hl = lane >> 5;
     const int key = min(kt + krow_key, T - 1);   // rows past T are masked after the product
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
-        t.k[kk] = *reinterpret_cast<const f16x8 *>(kb + key * ld + 16 * kk + 8 * hl);
-    if constexpr (ROPE) load_tables<D, ROPE>(cs, sn, row0 + key, hl, t.c, t.s);
+        t.k[kk] = *reinterpret_cast<const f16x8 *>(kb + key * ldk + 16 * kk + 8 * hl);
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) {
         const int e = lane + 64 * i;
         const int vkey = kt + e / VCH;
         // keys past T load as zero: their p is 0, and 0 * garbage could be NaN
-        t.v[i] = vkey < T ? *reinterpret_cast<const f16x8 *>(vb + vkey * ld + (e % VCH) * 8) : f16x8{};
+        t.v[i] = vkey < T ? *reinterpret_cast<const f16x8 *>(vb + vkey * ldv + (e % VCH) * 8) : f16x8{};
     }
 }
 
-// q, k, v rows are `ld` halves apart (H*D for separate tensors, 3*H*D inside
-// a fused [rows, 3, H, D] projection); out rows are H*D apart. With ROPE, the
-// rotary embedding (tables [rows, D]) is applied to q and k as they are loaded.
-template <int D, int WAVES, bool ROPE>
+// q and k rows are `ldqk` halves apart, v rows `ldv` (H*D for separate
+// tensors; 2*H*D and 3*H*D when q, k come from a [rows, 2, H, D] tensor and v
+// from a fused [rows, 3, H, D] projection); out rows are H*D apart.
+template <int D, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q, const f16 *__restrict__ k,
-                                                       const f16 *__restrict__ v, long long ld,
-                                                       f16 *__restrict__ o, const float *__restrict__ cs,
-                                                       const float *__restrict__ sn, int T, int H,
-                                                       float scale_log2e) {
+                                                       long long ldqk, const f16 *__restrict__ v, long long ldv,
+                                                       f16 *__restrict__ o, int T, int H, float scale_log2e) {
     constexpr int KC = D / 16;   // 16-wide d chunks of q.k
     constexpr int DT = D / 32;   // 32-row tiles of O^T
     constexpr int VCH = D / 8;   // 16-byte chunks per V row
@@ -136,8 +94,8 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     const int b = bh / H, h = bh % H;
     const long long ldo = (long long) H * D;   // output token stride
     const long long row0 = (long long) b * T;   // first row of this image
-    const f16 *qb = q + row0 * ld + (long long) h * D, *kb = k + row0 * ld + (long long) h * D,
-              *vb = v + row0 * ld + (long long) h * D;
+    const f16 *qb = q + row0 * ldqk + (long long) h * D, *kb = k + row0 * ldqk + (long long) h * D,
+              *vb = v + row0 * ldv + (long long) h * D;
     f16 *ob = o + row0 * ldo + (long long) h * D;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
     const int q0 = blockIdx.x * QT;
@@ -149,12 +107,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
         const int qi = min(q0 + c32, T - 1);
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk)
-            qf[kk] = *reinterpret_cast<const f16x8 *>(qb + qi * ld + 16 * kk + 8 * hl);
-        if constexpr (ROPE) {
-            float c[KC][8], sv[KC][8];
-            load_tables<D, ROPE>(cs, sn, row0 + qi, hl, c, sv);
-            rope_chunks<D>(qf, c, sv);
-        }
+            qf[kk] = *reinterpret_cast<const f16x8 *>(qb + qi * ldqk + 16 * kk + 8 * hl);
     }
     const int krow_key = kperm(c32);   // key (within a tile) this lane's K row holds
 
@@ -163,13 +116,12 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
     float m = -INFINITY, l = 0.f;
 
-    KvTile<D, ROPE> cur, nxt;
+    KvTile<D> cur, nxt;
     int kt = wave * KT;
-    if (kt < T) load_tile<D, ROPE>(kb, vb, cs, sn, ld, row0, T, kt, krow_key, lane, cur);
+    if (kt < T) load_tile<D>(kb, ldqk, vb, ldv, T, kt, krow_key, lane, cur);
     for (; kt < T; kt += WAVES * KT) {
         const int kn = kt + WAVES * KT;
-        if (kn < T) load_tile<D, ROPE>(kb, vb, cs, sn, ld, row0, T, kn, krow_key, lane, nxt);
-        if constexpr (ROPE) rope_chunks<D>(cur.k, cur.c, cur.s);
+        if (kn < T) load_tile<D>(kb, ldqk, vb, ldv, T, kn, krow_key, lane, nxt);
 
         // V tile -> wave-private LDS as V^T[d][key]
 #pragma unroll
@@ -257,9 +209,8 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     }
 }
 
-template <bool ROPE>
-void launch(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v, long long ld, hexlib_hf *out,
-            const float *cs, const float *sn, int rows, int H, int D, int batch, float scale) {
+void launch(const hexlib_hf *q, const hexlib_hf *k, long long ldqk, const hexlib_hf *v, long long ldv,
+            hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
     const int T = rows / batch;
     const dim3 grid((unsigned) ((T + QT - 1) / QT), (unsigned) (batch * H));
     const float sl2e = scale * 1.4426950408889634f;
@@ -267,8 +218,8 @@ void launch(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v, long lon
     const auto *K = reinterpret_cast<const f16 *>(k);
     const auto *V = reinterpret_cast<const f16 *>(v);
     auto *O = reinterpret_cast<f16 *>(out);
-    if (D == 64) HX_LAUNCH((attn_fwd<64, WAVES, ROPE>), grid, dim3(64 * WAVES), 0, Q, K, V, ld, O, cs, sn, T, H, sl2e);
-    else HX_LAUNCH((attn_fwd<32, WAVES, ROPE>), grid, dim3(64 * WAVES), 0, Q, K, V, ld, O, cs, sn, T, H, sl2e);
+    if (D == 64) HX_LAUNCH((attn_fwd<64, WAVES>), grid, dim3(64 * WAVES), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
+    else HX_LAUNCH((attn_fwd<32, WAVES>), grid, dim3(64 * WAVES), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
 }
 
 bool dims_ok(int rows, int H, int D, int batch) {
@@ -282,14 +233,14 @@ extern "C" void attention_fp16(const hexlib_hf *q, const hexlib_hf *k, const hex
                                hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
     if (!q || !k || !v || !out || !dims_ok(rows, H, D, batch)) return;
     if (!hx::aligned(q, 16) || !hx::aligned(k, 16) || !hx::aligned(v, 16) || !hx::aligned(out, 16)) return;
-    launch<false>(q, k, v, (long long) H * D, out, nullptr, nullptr, rows, H, D, batch, scale);
+    const long long hd = (long long) H * D;
+    launch(q, k, hd, v, hd, out, rows, H, D, batch, scale);
 }
 
-extern "C" void attention_qkv_rope_fp16(const hexlib_hf *qkv, const float *costab, const float *sintab,
-                                        hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
-    if (!qkv || !costab || !sintab || !out || !dims_ok(rows, H, D, batch)) return;
-    if (!hx::aligned(qkv, 16) || !hx::aligned(out, 16) || !hx::aligned(costab, 16) || !hx::aligned(sintab, 16))
-        return;
+extern "C" void attention_qk_v_fp16(const hexlib_hf *qk, const hexlib_hf *qkv, hexlib_hf *out,
+                                    int rows, int H, int D, int batch, float scale) {
+    if (!qk || !qkv || !out || !dims_ok(rows, H, D, batch)) return;
+    if (!hx::aligned(qk, 16) || !hx::aligned(qkv, 16) || !hx::aligned(out, 16)) return;
     const long long hd = (long long) H * D;
-    launch<true>(qkv, qkv + hd, qkv + 2 * hd, 3 * hd, out, costab, sintab, rows, H, D, batch, scale);
+    launch(qk, qk + hd, 2 * hd, qkv + 2 * hd, 3 * hd, out, rows, H, D, batch, scale);
 }

@@ -144,7 +144,8 @@ template <int V>
 __global__ __launch_bounds__(TPB) void rope_k(const f16 *__restrict__ x,
                                               const float *__restrict__ cs,
                                               const float *__restrict__ sn, f16 *__restrict__ y,
-                                              int T, int H, int D, long long total) {
+                                              int T, int H, int D, long long xld, long long yld,
+                                              long long total) {
 #pragma clang fp contract(off)
     const int half = D / 2;
     const int hv = half / V;
@@ -153,8 +154,9 @@ __global__ __launch_bounds__(TPB) void rope_k(const f16 *__restrict__ x,
         const int i = (int) (o % hv) * V;
         const long long th = o / hv;  // t*H + h
         const int t = (int) (th / H);
-        const f16 *xr = x + th * D;
-        f16 *yr = y + th * D;
+        const int hh = (int) (th % H);
+        const f16 *xr = x + t * xld + (long long) hh * D;
+        f16 *yr = y + t * yld + (long long) hh * D;
         const float *cr = cs + (long long) t * D;
         const float *sr = sn + (long long) t * D;
         float x0[V], x1[V], c0[V], c1[V], s0[V], s1[V];
@@ -252,20 +254,35 @@ extern "C" void patchify_fp32(const float *img, float *out, int C, int T, int H,
     patchify_fp32_batched(img, out, C, T, H, W, patch, merge, grid_h, grid_w, 1);
 }
 
-extern "C" void rope_2d_fp16(const hexlib_hf *x, const float *costab, const float *sintab,
-                             hexlib_hf *y, int T, int H, int D) {
-    if (T <= 0 || H <= 0 || D <= 0 || (D & 1) || !x || !costab || !sintab || !y) return;
+namespace {
+// rope over T tokens of H heads of D, token rows xld / yld halves apart.
+void rope_launch(const hexlib_hf *x, const float *costab, const float *sintab, hexlib_hf *y,
+                 int T, int H, int D, long long xld, long long yld) {
     auto X = reinterpret_cast<const f16 *>(x);
     auto Y = reinterpret_cast<f16 *>(y);
     const int half = D / 2;
-    if (half % 4 == 0 && hx::aligned(x, 8) && hx::aligned(y, 8) && hx::aligned(costab, 16) &&
-        hx::aligned(sintab, 16)) {
+    if (half % 4 == 0 && xld % 4 == 0 && yld % 4 == 0 && hx::aligned(x, 8) && hx::aligned(y, 8) &&
+        hx::aligned(costab, 16) && hx::aligned(sintab, 16)) {
         const long long total = (long long) T * H * (half / 4);
-        HX_LAUNCH(rope_k<4>, dim3(grid_for(total)), dim3(TPB), 0, X, costab, sintab, Y, T, H, D,
+        HX_LAUNCH(rope_k<4>, dim3(grid_for(total)), dim3(TPB), 0, X, costab, sintab, Y, T, H, D, xld, yld,
                   total);
     } else {
         const long long total = (long long) T * H * half;
-        HX_LAUNCH(rope_k<1>, dim3(grid_for(total)), dim3(TPB), 0, X, costab, sintab, Y, T, H, D,
+        HX_LAUNCH(rope_k<1>, dim3(grid_for(total)), dim3(TPB), 0, X, costab, sintab, Y, T, H, D, xld, yld,
                   total);
     }
+}
+}  // namespace
+
+extern "C" void rope_2d_fp16(const hexlib_hf *x, const float *costab, const float *sintab,
+                             hexlib_hf *y, int T, int H, int D) {
+    if (T <= 0 || H <= 0 || D <= 0 || (D & 1) || !x || !costab || !sintab || !y) return;
+    rope_launch(x, costab, sintab, y, T, H, D, (long long) H * D, (long long) H * D);
+}
+
+extern "C" void rope_2d_qk_fp16(const hexlib_hf *qkv, const float *costab, const float *sintab,
+                                hexlib_hf *qk, int rows, int H, int D) {
+    if (rows <= 0 || H <= 0 || D <= 0 || (D & 1) || !qkv || !costab || !sintab || !qk) return;
+    // q's H heads then k's H heads are 2H consecutive heads of each qkv row
+    rope_launch(qkv, costab, sintab, qk, rows, 2 * H, D, 3LL * H * D, 2LL * H * D);
 }

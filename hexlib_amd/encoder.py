@@ -16,8 +16,9 @@ Build extensions (not in the reference, each optional and off by default):
   reference's `rmsnorm_fp16` kernel contract.
 * `attention="fused"`: each block's attention chain (head transposes, scale,
   transpose_hd, two matmuls, softmax) as one `attention` op; `"fused_qkv_rope"`
-  additionally computes q, k, v with one [H, 3H] linear and applies rope_2d
-  inside the attention op (`fuse_qkv_feeds` rewrites reference feeds for it).
+  additionally computes q, k, v with one [H, 3H] linear, ropes q and k with one
+  `rope_2d_qk` op and reads v from the projection (`fuse_qkv_feeds` rewrites
+  reference feeds for it).
 
 Host-side tables (RoPE cos/sin, bilinear pos_embed) restate the reference
 loader (`hexlib/models/loader.py:30-146`).
@@ -54,8 +55,8 @@ class VitConfig:
     norm: str = "layernorm"
     batch: int = 1
     # "unfused": the reference graph; "fused": one attention op per block
-    # (KIND 18); "fused_qkv_rope": one q/k/v linear and one attention op that
-    # applies rope_2d itself (KIND 19)
+    # (KIND 18); "fused_qkv_rope": one q/k/v linear, one rope_2d_qk op on its q
+    # and k (KIND 20) and one attention op reading v from it (KIND 19)
     attention: str = "unfused"
 
     @property
@@ -237,7 +238,8 @@ def build_vision_encoder(cfg: VitConfig) -> Graph:
             fused = b.linear(a, f"{p}.wqkv", f"{p}.bqkv", H, 3 * H, f"{p}.qkv.out")
             qkv4 = b.emit("reshape", (fused,), f"{p}.qkv.h", (rows, 3, heads, d),
                           {"shape": (rows, 3, heads, d)})
-            ctxt = b.emit("attention", (qkv4, cos, sin), f"{p}.ctx.t", (rows, heads, d),
+            qk = b.emit("rope_2d_qk", (qkv4, cos, sin), f"{p}.qk.rope", (rows, 2, heads, d))
+            ctxt = b.emit("attention", (qk, qkv4), f"{p}.ctx.t", (rows, heads, d),
                           {"scale": float(d) ** -0.5, "batch": B})
         elif cfg.attention == "fused":
             # one op for the chain below; [rows, heads, d] in and out

@@ -47,7 +47,8 @@ KIND_ID: dict[str, int] = {
     "transpose_bth": 16,
     "matmul_epilogue_f16wt": 17,
     "attention": 18,
-    "attention_qkv_rope": 19,
+    "attention_qk_v": 19,
+    "rope_2d_qk": 20,
 }
 
 
@@ -273,19 +274,28 @@ SPECS: dict[str, RunnerSpec] = {
         checks=("D == 32 || D == 64", "rows % batch == 0", "(uint64_t)batch * H <= 65535",
                 "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
                 "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 15) == 0"),
-        weight=(1, "fp16"), rank=3,
+        rank=3,
         notes="extension: fused softmax(scale q k^T) v over [batch*T, H, D] q/k/v"),
-    "attention_qkv_rope": RunnerSpec(
-        "attention", "attention_qkv_rope_fp16", ("fp16", "fp32", "fp32"), "fp16",
+    "attention_qk_v": RunnerSpec(
+        "attention", "attention_qk_v_fp16", ("fp16", "fp16"), "fp16",
         (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),
          _S("attr:batch", "batch"), _S("attr:scale", "scale", "float")),
-        extents=("(uint64_t)rows*3*H*D", "(uint64_t)rows*D", "(uint64_t)rows*D", "(uint64_t)rows*H*D"),
-        checks=("a->ne[0][1] == 3", "D == 32 || D == 64", "rows % batch == 0",
-                "(uint64_t)batch * H <= 65535",
+        extents=("(uint64_t)rows*2*H*D", "(uint64_t)rows*3*H*D", "(uint64_t)rows*H*D"),
+        checks=("a->ne[0][1] == 2", "a->ne[1][0] == a->ne[0][0]", "a->ne[1][1] == 3",
+                "a->ne[1][2] == a->ne[0][2]", "a->ne[1][3] == a->ne[0][3]",
+                "D == 32 || D == 64", "rows % batch == 0", "(uint64_t)batch * H <= 65535",
                 "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
-                "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 15) == 0"),
-        weight=(1, "fp32"), rank=4, primary=False,
-        notes="extension: attention over a fused [rows, 3, H, D] QKV projection, rope_2d on q and k"),
+                "((uintptr_t)a->buf[2] & 15) == 0"),
+        rank=4,
+        notes="extension: attention with q, k from rope_2d_qk's [rows, 2, H, D] and v from the "
+              "fused [rows, 3, H, D] projection"),
+    "rope_2d_qk": RunnerSpec(
+        "rope_2d_qk", "rope_2d_qk_fp16", ("fp16", "fp32", "fp32"), "fp16",
+        (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D")),
+        extents=("(uint64_t)rows*3*H*D", "(uint64_t)rows*D", "(uint64_t)rows*D", "(uint64_t)rows*2*H*D"),
+        checks=("a->ne[0][1] == 3", "D % 2 == 0"),
+        rank=4,
+        notes="extension: rope_2d on the q and k parts of a fused [rows, 3, H, D] projection"),
 }
 
 
@@ -312,7 +322,8 @@ def select(kind: str, attrs: Mapping[str, Any], in_dtypes: Sequence[str] | None 
     ok = [(n, s) for n, s in cands if s.accepts(attrs)]
     if in_dtypes is not None:
         ok = [(n, s) for n, s in ok
-              if s.weight is None or in_dtypes[s.weight[0]] == s.weight[1]]
+              if len(s.inputs) == len(in_dtypes)
+              and (s.weight is None or in_dtypes[s.weight[0]] == s.weight[1])]
     if weight_layout is not None and len(ok) > 1:
         narrowed = [(n, s) for n, s in ok
                     if s.weight is None or s.buf_layouts()[s.weight[0]] == weight_layout]

@@ -115,26 +115,35 @@ def _rope_infer(inputs, attrs):
 
 
 def _attention_infer(inputs, attrs):
-    """(q, k, v) each [rows, heads, head_dim]; or (qkv [rows, 3, heads,
-    head_dim], cos, sin [rows, head_dim]) with the rotary embedding applied to
-    q and k first. Output [rows, heads, head_dim]."""
-    if len(inputs[0].shape) == 4:
-        qkv, cos, sin = inputs
-        rows, three, heads, d = qkv.shape
-        if three != 3 or cos.shape != (rows, d) or sin.shape != (rows, d) or d % 2:
-            raise ValueError(f"attention over fused qkv {qkv.shape} with tables {cos.shape}/{sin.shape}")
-        batch = int(attrs.get("batch", 1))
-        if batch < 1 or rows % batch:
-            raise ValueError(f"attention: {rows} rows do not split into {batch} images")
-        return (((rows, heads, d), qkv.dtype),)
-    q, k, v = inputs
-    if len(q.shape) != 3 or q.shape != k.shape or q.shape != v.shape:
-        raise ValueError(f"attention wants q, k, v of one [rows, heads, head_dim] shape, "
-                         f"got {q.shape} {k.shape} {v.shape}")
+    """(q, k, v) each [rows, heads, head_dim]; or (qk [rows, 2, heads,
+    head_dim], qkv [rows, 3, heads, head_dim]): q, k from the first, v from
+    the third slot of the second. Output [rows, heads, head_dim]."""
     batch = int(attrs.get("batch", 1))
-    if batch < 1 or q.shape[0] % batch:
-        raise ValueError(f"attention: {q.shape[0]} rows do not split into {batch} images")
-    return ((q.shape, q.dtype),)
+    if len(inputs) == 2:
+        qk, qkv = inputs
+        rows, two, heads, d = qk.shape if len(qk.shape) == 4 else (0, 0, 0, 0)
+        if two != 2 or qkv.shape != (rows, 3, heads, d):
+            raise ValueError(f"attention over qk {qk.shape} and qkv {qkv.shape}")
+        out = (rows, heads, d)
+    else:
+        q, k, v = inputs
+        if len(q.shape) != 3 or q.shape != k.shape or q.shape != v.shape:
+            raise ValueError(f"attention wants q, k, v of one [rows, heads, head_dim] shape, "
+                             f"got {q.shape} {k.shape} {v.shape}")
+        out = q.shape
+    if batch < 1 or out[0] % batch:
+        raise ValueError(f"attention: {out[0]} rows do not split into {batch} images")
+    return ((out, inputs[0].dtype),)
+
+
+def _rope_qk_infer(inputs, attrs):
+    qkv, cos, sin = inputs
+    if len(qkv.shape) != 4 or qkv.shape[1] != 3:
+        raise ValueError(f"rope_2d_qk wants a fused [rows, 3, heads, head_dim] projection, got {qkv.shape}")
+    rows, _, heads, d = qkv.shape
+    if cos.shape != (rows, d) or sin.shape != (rows, d) or d % 2:
+        raise ValueError(f"rope tables {cos.shape}/{sin.shape} vs qkv {qkv.shape}")
+    return (((rows, 2, heads, d), qkv.dtype),)
 
 
 for _kind, _fn in (
@@ -153,5 +162,6 @@ for _kind, _fn in (
     ("patchify", _patchify_infer),
     ("rope_2d", _rope_infer),
     ("attention", _attention_infer),
+    ("rope_2d_qk", _rope_qk_infer),
 ):
     register(OpDef(kind=_kind, infer=_fn))

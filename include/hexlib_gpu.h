@@ -9,7 +9,7 @@
  *     dimensions make the call a silent no-op, as in the reference.
  *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
  *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
- *     KIND_ID (1-12) plus appended ids 13-19. Generated from the host's
+ *     KIND_ID (1-12) plus appended ids 13-20. Generated from the host's
  *     RunnerSpec table (hexlib_amd/exec/genentry.py).
  *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
  *     stop/close/hwinfo) that validates a batch blob on the host, resolves
@@ -210,16 +210,18 @@ void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
  * and out are 16-byte aligned. */
 void attention_fp16(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v,
                     hexlib_hf *out, int rows, int H, int D, int batch, float scale);
-/* Fused attention over a fused QKV projection, with the rotary embedding
- * (KIND 19): qkv is [rows, 3, H, D] fp16 (q, k, v of each token side by side,
- * the output of one [K, 3*H*D] linear); rope_2d_fp16's split-half rotation
- * with fp32 tables cos/sin [rows, D] is applied to q and k (each rotated value
- * rounded to fp16, as rope_2d_fp16 stores it) before attention_fp16's
- * computation; out is [rows, H, D]. Replaces the three q/k/v linears' reshape,
- * the two rope_2d ops and attention_fp16's chain. No-op unless rows % batch == 0
- * and every pointer is 16-byte aligned. */
-void attention_qkv_rope_fp16(const hexlib_hf *qkv, const float *costab, const float *sintab,
-                             hexlib_hf *out, int rows, int H, int D, int batch, float scale);
+/* rope_2d_fp16 on the q and k parts of a fused projection (KIND 20): qkv is
+ * [rows, 3, H, D] fp16 (q, k, v of each token side by side, the output of one
+ * [K, 3*H*D] linear); qk is [rows, 2, H, D] = (rope(q), rope(k)), with
+ * rope_2d_fp16's arithmetic and fp32 tables cos/sin [rows, D]. */
+void rope_2d_qk_fp16(const hexlib_hf *qkv, const float *costab, const float *sintab,
+                     hexlib_hf *qk, int rows, int H, int D);
+/* attention_fp16 with q and k taken from qk [rows, 2, H, D] (rope_2d_qk_fp16's
+ * output) and v from the fused projection qkv [rows, 3, H, D] (KIND 19);
+ * out [rows, H, D]. No-op unless rows % batch == 0 and every pointer is
+ * 16-byte aligned. */
+void attention_qk_v_fp16(const hexlib_hf *qk, const hexlib_hf *qkv, hexlib_hf *out,
+                         int rows, int H, int D, int batch, float scale);
 
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
@@ -239,7 +241,8 @@ int matmul_epilogue_f16w_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q4k_fp16_entry(const hexlib_args *a);
 int attention_fp16_entry(const hexlib_args *a);
-int attention_qkv_rope_fp16_entry(const hexlib_args *a);
+int attention_qk_v_fp16_entry(const hexlib_args *a);
+int rope_2d_qk_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

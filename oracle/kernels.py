@@ -24,7 +24,8 @@ any summation order the GPU picks.
 | matmul_epilogue_f16w | hexlib/graph/opdefs/fused.py:44-53 with fp16 w    | reduces to matmul_epilogue_fp16 on dequantized weights |
 | matmul_q4k           | q4_0 blocks along K of W^T, same numerics as q4_0 | reduces to matmul_epilogue_fp16 via a block transpose |
 | attention_fp16       | hexlib/models/vit.py:185-193 chain, fused         | equals the composition of the registry references; uniform / one-hot closed forms |
-| attention_qkv_rope_fp16 | rope_2d_fp16 on q, k, then attention_fp16      | composition of the two pinned functions above |
+| rope_2d_qk_fp16      | rope_2d_fp16 on the q, k slots of a fused qkv     | rope_2d_fp16 (pinned bit-exact) per slot |
+| attention_qk_v_fp16  | attention_fp16 on strided q, k, v                 | attention_fp16 |
 """
 from __future__ import annotations
 
@@ -164,10 +165,13 @@ def attention_fp16(q, k, v, batch, scale):
     return o.astype(np.float16)
 
 
-def attention_qkv_rope_fp16(qkv, cos, sin, batch, scale):
-    """The fused-projection form: rope_2d_fp16 (with its fp16 rounding) on q
-    and k, then attention_fp16."""
+def rope_2d_qk_fp16(qkv, cos, sin):
+    """rope_2d_fp16 on the q and k slots of [rows, 3, H, D] -> [rows, 2, H, D]."""
     qkv = np.asarray(qkv, np.float16)
-    q = rope_2d_fp16(np.ascontiguousarray(qkv[:, 0]), cos, sin)
-    k = rope_2d_fp16(np.ascontiguousarray(qkv[:, 1]), cos, sin)
-    return attention_fp16(q, k, np.ascontiguousarray(qkv[:, 2]), batch, scale)
+    return np.stack([rope_2d_fp16(np.ascontiguousarray(qkv[:, j]), cos, sin) for j in (0, 1)], axis=1)
+
+
+def attention_qk_v_fp16(qk, qkv, batch, scale):
+    """attention_fp16 with q, k from qk [rows, 2, H, D] and v from qkv [rows, 3, H, D]."""
+    qk, qkv = np.asarray(qk, np.float16), np.asarray(qkv, np.float16)
+    return attention_fp16(qk[:, 0], qk[:, 1], qkv[:, 2], batch, scale)

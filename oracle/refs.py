@@ -122,13 +122,11 @@ def attention(arrays, attrs):
     (`hexlib/models/vit.py:185-193`: scale, transpose_hd, matmul, softmax,
     matmul, with the head transposes around it) computed in float64 with no
     intermediate storage rounding; q, k, v, out are [batch*T, H, D]. The fused-
-    projection form takes (qkv [batch*T, 3, H, D], cos, sin) and applies the
-    rope_2d reference (float32, structural.py:240-254) to q and k first."""
-    if np.ndim(arrays[0]) == 4:   # (qkv [rows, 3, H, D], cos, sin): rope_2d on q and k first
-        qkv, cos, sin = arrays
-        (qr,) = rope_2d((qkv[:, 0], cos, sin), {})
-        (kr,) = rope_2d((qkv[:, 1], cos, sin), {})
-        arrays = (qr, kr, qkv[:, 2])
+    projection form takes (qk [batch*T, 2, H, D], qkv [batch*T, 3, H, D]):
+    q and k from the first, v from the third slot of the second."""
+    if len(arrays) == 2:   # (qk [rows, 2, H, D], qkv [rows, 3, H, D])
+        qk, qkv = arrays
+        arrays = (qk[:, 0], qk[:, 1], qkv[:, 2])
     q, k, v = (np.asarray(a, np.float64) for a in arrays)
     batch = int(attrs.get("batch", 1))
     rows, heads, d = q.shape
@@ -143,10 +141,19 @@ def attention(arrays, attrs):
     return (o.transpose(0, 2, 1, 3).reshape(rows, heads, d).astype(arrays[0].dtype),)
 
 
+def rope_2d_qk(arrays, attrs):
+    """rope_2d (structural.py:240-254) on the q and k slots of a fused
+    [rows, 3, H, D] projection -> [rows, 2, H, D]."""
+    qkv, cos, sin = arrays
+    (q,) = rope_2d((qkv[:, 0], cos, sin), {})
+    (k,) = rope_2d((qkv[:, 1], cos, sin), {})
+    return (np.stack([q, k], axis=1),)
+
+
 REFERENCES = {
     "add": add, "scale": scale, "layernorm": layernorm, "rmsnorm": rmsnorm,
     "gelu_tanh": gelu_tanh, "gelu_erf": gelu_erf, "softmax": softmax,
     "matmul": matmul, "matmul_epilogue": matmul_epilogue, "cast": cast,
     "transpose": transpose, "reshape": reshape, "patchify": patchify,
-    "rope_2d": rope_2d, "attention": attention,
+    "rope_2d": rope_2d, "attention": attention, "rope_2d_qk": rope_2d_qk,
 }

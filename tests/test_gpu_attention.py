@@ -71,29 +71,38 @@ def test_attention_invalid_is_a_silent_no_op(dev):
     assert (dev.down(do) == np.float16(12345.0)).all()
 
 
-@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (2, 33, 2, 64), (3, 17, 2, 32)])
-def test_attention_qkv_rope(dev, B, T, H, D):
-    """KIND 19: q, k, v side by side in one [rows, 3, H, D] projection, rope_2d
-    on q and k inside the kernel. Oracle: rope_2d_fp16 (pinned bit-exact
-    against the reference baseline) then attention."""
-    from hexlib_amd import encoder as E
+def _tables(r, rows, T, H, D, B):
     from dataclasses import replace
-    r = np.random.default_rng(80 + T)
-    rows = B * T
-    qkv = h16(r.standard_normal((rows, 3, H, D)))
+    from hexlib_amd import encoder as E
     grid = int(round(np.sqrt(T)))
     if grid * grid == T:
         cfg = replace(E.QWEN35_VISION_FP16, image_size=16 * grid, hidden_size=H * D, num_heads=H, batch=B)
-        cos, sin = E.rope_tables(cfg)
-    else:
-        ang = r.random((rows, D // 2)) * 6.0
-        cos = np.concatenate([np.cos(ang)] * 2, axis=1).astype(np.float32)
-        sin = np.concatenate([np.sin(ang)] * 2, axis=1).astype(np.float32)
+        return E.rope_tables(cfg)
+    ang = r.random((rows, D // 2)) * 6.0
+    return (np.concatenate([np.cos(ang)] * 2, axis=1).astype(np.float32),
+            np.concatenate([np.sin(ang)] * 2, axis=1).astype(np.float32))
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (2, 33, 2, 64), (3, 17, 2, 32)])
+def test_rope_2d_qk_and_attention_qk_v(dev, B, T, H, D):
+    """KIND 20 then KIND 19: rope_2d on the q and k slots of one fused
+    [rows, 3, H, D] projection (bit-exact against rope_2d_fp16, itself pinned
+    bit-exact against the reference baseline), then attention with q, k from
+    its output and v from the projection."""
+    r = np.random.default_rng(80 + T)
+    rows = B * T
+    qkv = h16(r.standard_normal((rows, 3, H, D)))
+    cos, sin = _tables(r, rows, T, H, D, B)
     dqkv, dc, ds = dev.up(qkv), dev.up(cos), dev.up(sin)
+    dqk = dev.empty((rows, 2, H, D), np.float16)
+    dev.lib.rope_2d_qk_fp16(dev.ptr(dqkv), dev.ptr(dc), dev.ptr(ds), dev.ptr(dqk), rows, H, D)
+    dev.check()
+    qk = dev.down(dqk)
+    np.testing.assert_array_equal(qk.view(np.uint16), K.rope_2d_qk_fp16(qkv, cos, sin).view(np.uint16))
     do = dev.empty((rows, H, D), np.float16)
-    dev.lib.attention_qkv_rope_fp16(dev.ptr(dqkv), dev.ptr(dc), dev.ptr(ds), dev.ptr(do), rows, H, D, B, D ** -0.5)
+    dev.lib.attention_qk_v_fp16(dev.ptr(dqk), dev.ptr(dqkv), dev.ptr(do), rows, H, D, B, D ** -0.5)
     dev.check()
     got = dev.down(do)
-    want = K.attention_qkv_rope_fp16(qkv, cos, sin, B, D ** -0.5)
-    report(f"attention_qkv_rope B{B} T{T} H{H} D{D}", got, want)
+    want = K.attention_qk_v_fp16(qk, qkv, B, D ** -0.5)
+    report(f"attention_qk_v B{B} T{T} H{H} D{D}", got, want)
     assert K.close_f16(got, want, 1e-2, 1e-3).all()

@@ -229,7 +229,7 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     cfg = replace(cfg_ref, attention=mode)
     fused_feeds = E.fuse_qkv_feeds(feeds, cfg) if mode == "fused_qkv_rope" else feeds
     (out,), wb = _run_plan(session, cfg, fused_feeds, graph_mode=True)
-    assert wb.n_ops == 259 - 12 * (8 if mode == "fused" else 12)
+    assert wb.n_ops == 259 - 12 * (8 if mode == "fused" else 11)
     want = _oracle(cfg_ref, feeds)
     err = np.abs(out - want).max()
     print(f"[{mode} {image} b{batch}] max abs vs reference graph {err:.3e}", flush=True)

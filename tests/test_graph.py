@@ -185,10 +185,11 @@ def test_fused_attention_plan():
                 _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope", batch=2)):
         g = E.build_vision_encoder(cfg)
         wb = WP.build_whole_plan_batch(g, E.synthetic_feeds(g, cfg))
-        assert wb.n_ops == 259 - 12 * 12       # and two fewer linears, no rope ops
-        assert sum(1 for s in wb.op_specs if s == "attention_qkv_rope") == 12
+        assert wb.n_ops == 259 - 12 * 11       # two fewer linears, one rope op instead of two
+        assert sum(1 for s in wb.op_specs if s == "attention_qk_v") == 12
+        assert sum(1 for s in wb.op_specs if s == "rope_2d_qk") == 12
         assert not any(s == "rope_2d" for s in wb.op_specs)
-        assert KIND_ID["attention_qkv_rope"] == 19
+        assert KIND_ID["attention_qk_v"] == 19 and KIND_ID["rope_2d_qk"] == 20
 
 
 def test_fused_qkv_feeds_compute_the_reference_function():

@@ -265,16 +265,16 @@ def test_attention_entry_checks(sess, rows, H, D, batch, align_out, want):
     assert sess.invoke(blob)[0] == wire.STATUS[want]
 
 
-@pytest.mark.parametrize("three,D,want", [(3, 64, "OK"), (2, 64, "ERR_INVAL_PARAMS"), (3, 40, "ERR_INVAL_PARAMS")])
-def test_attention_qkv_rope_entry_checks(sess, three, D, want):
+@pytest.mark.parametrize("two,three,D,want", [(2, 3, 64, "OK"), (3, 3, 64, "ERR_INVAL_PARAMS"),
+                                              (2, 2, 64, "ERR_INVAL_PARAMS"), (2, 3, 40, "ERR_INVAL_PARAMS")])
+def test_attention_qk_v_entry_checks(sess, two, three, D, want):
     rows, H = 64, 2
-    sizes = [rows * three * H * D * 2, rows * D * 4, rows * D * 4, rows * H * D * 2]
+    sizes = [rows * two * H * D * 2, rows * three * H * D * 2, rows * H * D * 2]
     offs = np.cumsum([0] + [(x + 255) // 256 * 256 for x in sizes])
-    t = [wire.TensorDesc(0, int(offs[0]), sizes[0], "fp16", "row_major", (rows, three, H, D)),
-         wire.TensorDesc(0, int(offs[1]), sizes[1], "fp32", "row_major", (rows, D, 1, 1)),
-         wire.TensorDesc(0, int(offs[2]), sizes[2], "fp32", "row_major", (rows, D, 1, 1)),
-         wire.TensorDesc(0, int(offs[3]), sizes[3], "fp16", "row_major", (rows, H, D, 1))]
-    op = wire.OpDesc(KIND_ID["attention_qkv_rope"], (1, wire.float_param(0.125)), (0, 1, 2), (3,))
-    blob = wire.pack_batch([wire.BufDesc(3, int(offs[4]))], t, [op])
-    assert sess.mmap(3, int(offs[4])) == OK
+    t = [wire.TensorDesc(0, int(offs[0]), sizes[0], "fp16", "row_major", (rows, two, H, D)),
+         wire.TensorDesc(0, int(offs[1]), sizes[1], "fp16", "row_major", (rows, three, H, D)),
+         wire.TensorDesc(0, int(offs[2]), sizes[2], "fp16", "row_major", (rows, H, D, 1))]
+    op = wire.OpDesc(KIND_ID["attention_qk_v"], (1, wire.float_param(0.125)), (0, 1), (2,))
+    blob = wire.pack_batch([wire.BufDesc(3, int(offs[3]))], t, [op])
+    assert sess.mmap(3, int(offs[3])) == OK
     assert sess.invoke(blob)[0] == wire.STATUS[want]
