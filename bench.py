@@ -83,12 +83,15 @@ def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
 
 # ---- plan helpers -------------------------------------------------------------------------
 
-def build_plan(cfg, seed=0, weight_layout="auto"):
+def build_plan(cfg, seed=0, weight_layout="auto", residual=True):
+    """The product plan: fusions on (`residual` folds residual adds into the
+    fp16 linears; the config's `attention` picks the attention form)."""
     from hexlib_amd import encoder as E
     from hexlib_amd.exec.wholeplan import build_whole_plan_batch
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=seed)
-    return g, feeds, build_whole_plan_batch(g, feeds, weight_layout=weight_layout)
+    return g, feeds, build_whole_plan_batch(g, feeds, weight_layout=weight_layout,
+                                            residual=residual and cfg.attention != "unfused")
 
 
 def time_replays(plan, steps: int, warmup: int) -> float:
@@ -109,13 +112,8 @@ def time_replays(plan, steps: int, warmup: int) -> float:
 
 def unique_ops(g, wb):
     """(spec, input shapes/dtypes, output) -> [count, first op desc index]."""
-    from hexlib_amd.graph.fuse import fuse
-    f = fuse(g)
     out = {}
-    i = 0
-    for op in f.ops:
-        if op.kind == "reshape":
-            continue
+    for i, op in enumerate(wb.graph_ops):
         spec = wb.op_specs[i]
         ins = tuple((wb.placements[n].shape, wb.placements[n].dtype) for n in op.inputs)
         if spec.startswith("attention"):
@@ -125,7 +123,6 @@ def unique_ops(g, wb):
         if key not in out:
             out[key] = [0, i, op]
         out[key][0] += 1
-        i += 1
     return out
 
 
@@ -176,12 +173,17 @@ def per_op_in_plan(plan, g, reps: int = 40) -> list[dict]:
 # ---- roofline of the dominant kernel ---------------------------------------------------
 
 def dominant_op(g, wb):
-    """The plan's GEMM shape with the most launches per image (ties: first in
-    plan order). For the cfg-4 encoder this is the 256x768x768 W^T linear (QKV
-    thirds, proj, merger input): 49 launches per image."""
-    rows = [(count, -idx, spec, ins, out) for (spec, ins, out), (count, idx, _) in unique_ops(g, wb).items()
-            if spec.startswith("matmul_epilogue")]
-    count, neg_idx, spec, ins, out = max(rows)
+    """The plan's GEMM row with the most algorithmic work per image (launches
+    x FLOPs; ties: first in plan order). For the cfg-4 encoder plan that is
+    the MLP up-projection fc1, 256x768x3072 (12 launches, tied with fc2 in
+    work; fc1 runs as one kernel, fc2 as split-K partials plus a reduction)."""
+    rows = []
+    for (spec, ins, out), (count, idx, _) in unique_ops(g, wb).items():
+        if not spec.startswith("matmul_epilogue"):
+            continue
+        flops = op_work(spec, [s for s, _ in ins], out[0], [d for _, d in ins], out[1])[1]
+        rows.append((count * flops, -idx, spec, ins, out, count))
+    work, neg_idx, spec, ins, out, count = max(rows)
     return {"spec": spec, "index": -neg_idx, "count": count, "inputs": ins, "output": out}
 
 
@@ -200,7 +202,7 @@ def roofline(plan, g, reps: int = 200, iters: int = 7) -> dict:
     ridge = MFMA_FP16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     ai = flops / nbytes
     m, k = shapes[0]
-    n = shapes[1][0] if d["spec"].endswith("f16wt") else shapes[1][-1]
+    n = oshape[-1]
     out = {"kernel": f"{d['spec']} {m}x{k}x{n}", "launches_per_image": d["count"],
            "avg_launch_ns": round(ns, 1), "algorithmic_bytes": int(nbytes), "flops": int(flops),
            "arith_intensity": round(ai, 1)}

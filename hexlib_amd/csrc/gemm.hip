@@ -61,7 +61,19 @@ struct GemmArgs {
     int M, N, K, act;
     int splits, k_per_split;    // split-K: K range [s*k_per_split, min(K, (s+1)*k_per_split))
     float *ws;                  // split-K workspace [batch][splits][M][N] fp32
+    const f16 *R;               // residual [M, N] (row stride ldr) added after rounding, or null
+    long long ldr;
 };
+
+// One output's epilogue: act(acc + bias) rounded to fp16 and, with a residual
+// r, fp16(float(r) + float(that)) -- matmul_epilogue then add_fp16, each
+// rounded as the reference stores it (the sum is materialised in fp32 first,
+// so the compiler cannot fuse it into the fp16 conversion).
+__device__ __forceinline__ f16 epi(float v, int act, const f16 *r) {
+    const f16 h = (f16) apply_act(v, act);
+    if (!r) return h;
+    return (f16) f32_rounded((float) *r + (float) h);
+}
 
 __device__ __forceinline__ f16 q4_val(float d, int q) { return (f16) (d * (float) (q - 8)); }
 
@@ -344,12 +356,14 @@ struct Gemm {
                     if (vec_store && n + 3 < p.N) {
                         f16x4 o;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) o[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                        for (int e = 0; e < 4; ++e)
+                            o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
                         *reinterpret_cast<f16x4 *>(dst) = o;
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            if (n + e < p.N) dst[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                            if (n + e < p.N)
+                                dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
                     }
                 }
             }
@@ -527,12 +541,14 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
                 if (vec_store && n + 3 < p.N) {
                     f16x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                    for (int e = 0; e < 4; ++e)
+                        o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
                     *reinterpret_cast<f16x4 *>(dst) = o;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (n + e < p.N) dst[e] = (f16) apply_act(acc[j][i][g * 4 + e] + bv[e], p.act);
+                        if (n + e < p.N)
+                            dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
                 }
             }
         }
@@ -544,7 +560,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
 __global__ __launch_bounds__(TPB) void splitk_reduce(const float *__restrict__ ws,
                                                      const float *__restrict__ bias,
                                                      f16 *__restrict__ C, long long ldc, long long sC,
-                                                     int M, int N, int splits, int act, int batch) {
+                                                     int M, int N, int splits, int act, int batch,
+                                                     const f16 *__restrict__ R, long long ldr) {
     const long long per = (long long) M * N;
     const long long quads = (per + 3) / 4;
     const long long total = quads * batch;
@@ -577,7 +594,8 @@ __global__ __launch_bounds__(TPB) void splitk_reduce(const float *__restrict__ w
             if (o >= per) break;
             const int m = (int) (o / N), n = (int) (o % N);
             const float b = bias ? bias[n] : 0.0f;
-            C[(long long) bz * sC + (long long) m * ldc + n] = (f16) apply_act(s[e] + b, act);
+            C[(long long) bz * sC + (long long) m * ldc + n] =
+                epi(s[e] + b, act, R ? R + (long long) m * ldr + n : nullptr);
         }
     }
 }
@@ -708,7 +726,7 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     if (p.splits > 1) {
         const long long quads = ((long long) p.M * p.N + 3) / 4 * batch;
         HX_LAUNCH(splitk_reduce, dim3(hx::blocks_for(quads, TPB, 4096)), dim3(TPB), 0,
-                  (const float *) p.ws, p.bias, p.C, p.ldc, p.sC, p.M, p.N, p.splits, p.act, batch);
+                  (const float *) p.ws, p.bias, p.C, p.ldc, p.sC, p.M, p.N, p.splits, p.act, batch, p.R, p.ldr);
     }
 }
 
@@ -785,6 +803,16 @@ extern "C" void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *
     if (!a || !wt || !out || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
     launch<B_NK>(args(a, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act), 1,
                  K % 8 == 0 && hx::aligned(a, 16), K % 8 == 0 && hx::aligned(wt, 16));
+}
+
+extern "C" void matmul_epilogue_f16wt_res_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
+                                               const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N,
+                                               int act) {
+    if (!a || !wt || !resid || !out || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
+    GemmArgs p = args(a, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act);
+    p.R = reinterpret_cast<const f16 *>(resid);
+    p.ldr = N;
+    launch<B_NK>(p, 1, K % 8 == 0 && hx::aligned(a, 16), K % 8 == 0 && hx::aligned(wt, 16));
 }
 
 extern "C" void matmul_epilogue_fp16(const hexlib_hf *a, const unsigned char *w, const float *bias,

@@ -49,6 +49,7 @@ KIND_ID: dict[str, int] = {
     "attention": 18,
     "attention_qk_v": 19,
     "rope_2d_qk": 20,
+    "matmul_epilogue_f16wt_res": 21,
 }
 
 
@@ -276,6 +277,14 @@ SPECS: dict[str, RunnerSpec] = {
                 "((uintptr_t)a->buf[2] & 15) == 0", "((uintptr_t)a->buf[3] & 15) == 0"),
         rank=3,
         notes="extension: fused softmax(scale q k^T) v over [batch*T, H, D] q/k/v"),
+    "matmul_epilogue_f16wt_res": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_f16wt_res_fp16", ("fp16", "fp16", "fp32", "fp16"), "fp16",
+        _MM_SCALARS,
+        layouts=("row_major", "col_major", "row_major", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N", "(uint64_t)M*N"),
+        weight=(1, "fp16"), primary=False, rank=2,
+        notes="extension: a linear with the residual add that consumes it folded into the "
+              "epilogue (fused by hexlib_amd.graph.fuse.fuse_residual); fp16 W^T only"),
     "attention_qk_v": RunnerSpec(
         "attention", "attention_qk_v_fp16", ("fp16", "fp16"), "fp16",
         (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),

@@ -32,7 +32,7 @@ import numpy as np
 
 from hexlib_amd.exec import wire
 from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, RunnerSpec, select
-from hexlib_amd.graph.fuse import fuse
+from hexlib_amd.graph.fuse import fuse, fuse_residual
 from hexlib_amd.graph.ir import Graph
 from hexlib_amd.graph.ir import nbytes as ir_nbytes
 from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
@@ -75,6 +75,7 @@ class WholePlanBatch:
     op_names: tuple[str, ...] = field(default=())
     op_specs: tuple[str, ...] = field(default=())
     const_bytes: int = 0
+    graph_ops: tuple = field(default=())   # the plan's non-reshape graph ops, in wire order
 
 
 def _spec_for(op, graph: Graph, weight_layout: str | None) -> tuple[str, RunnerSpec]:
@@ -131,8 +132,13 @@ def _reuse_offsets(g: Graph, acts, reshape_src, owner, wbytes) -> tuple[dict[str
 
 def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                            weight_layout: str | None = "auto", fuse_first: bool = True,
-                           fd: int = 0, reuse: bool = True) -> WholePlanBatch:
+                           fd: int = 0, reuse: bool = True, residual: bool = False) -> WholePlanBatch:
+    """`residual=True` also folds each residual add into the fp16 linear that
+    feeds it (`fuse_residual`), when fp16 weights are staged transposed (the
+    only layout with that kernel)."""
     g = fuse(graph) if fuse_first else graph
+    if residual and weight_layout in ("auto", "col_major"):
+        g = fuse_residual(g)
     tensors = g.tensors
     io = set(g.inputs) | set(g.outputs)
     consts = {n for n, t in tensors.items() if t.const}
@@ -246,12 +252,13 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
     wtensors = [wire.TensorDesc(0, placements[n].offset, placements[n].nbytes,
                                 placements[n].dtype, placements[n].layout, placements[n].ne)
                 for n in order]
-    ops, names, specs = [], [], []
+    ops, names, specs, gops = [], [], [], []
     skipped = 0
     for op in g.ops:
         if op.kind == "reshape":
             skipped += 1
             continue
+        gops.append(op)
         spec_name, spec = op_specs[op.id]
         shapes = [tensors[n].shape for n in op.inputs]
         ops.append(wire.OpDesc(kind=KIND_ID[spec_name], params=spec.params(shapes, op.attrs),
@@ -263,7 +270,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
     return WholePlanBatch(blob=blob, payload=payload, placements=placements, index=index,
                           n_ops=len(ops), arena_bytes=arena, outputs=tuple(g.outputs),
                           inputs=tuple(g.inputs), skipped_reshapes=skipped,
-                          op_names=tuple(names), op_specs=tuple(specs), const_bytes=const_end)
+                          op_names=tuple(names), op_specs=tuple(specs), const_bytes=const_end,
+                          graph_ops=tuple(gops))
 
 
 def decode(batch: WholePlanBatch, name: str, raw: bytes) -> np.ndarray:

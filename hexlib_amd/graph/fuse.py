@@ -77,3 +77,40 @@ def fuse(graph: Graph) -> Graph:
     ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
     tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
     return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)
+
+
+def fuse_residual(graph: Graph) -> Graph:
+    readers: dict[str, list[Op]] = {}
+    for op in graph.ops:
+        for name in op.inputs:
+            readers.setdefault(name, []).append(op)
+    outputs = set(graph.outputs)
+    absorbed: set[int] = set()
+    replaced: dict[int, Op] = {}
+    dropped: set[str] = set()
+    for op in graph.ops:
+        if op.kind != "matmul_epilogue" or len(op.inputs) != 3 or op.id in absorbed:
+            continue
+        if graph.tensor(op.inputs[1]).dtype != "fp16":
+            continue
+        out = op.outputs[0]
+        rd = readers.get(out, [])
+        if out in outputs or len(rd) != 1 or rd[0].kind != "add" or rd[0].id in absorbed:
+            continue
+        add = rd[0]
+        other = [n for n in add.inputs if n != out]
+        if len(add.inputs) != 2 or len(other) != 1:
+            continue
+        res = graph.tensor(other[0])
+        if res.const or res.shape != graph.tensor(out).shape or res.dtype != graph.tensor(out).dtype:
+            continue
+        replaced[op.id] = Op(id=op.id, kind="matmul_epilogue",
+                             inputs=op.inputs + (other[0],), outputs=add.outputs,
+                             attrs={**dict(op.attrs), "round": graph.tensor(out).dtype})
+        absorbed.add(add.id)
+        dropped.add(out)
+    if not replaced:
+        return graph
+    ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
+    tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
+    return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)

@@ -9,7 +9,7 @@
  *     dimensions make the call a silent no-op, as in the reference.
  *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
  *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
- *     KIND_ID (1-12) plus appended ids 13-20. Generated from the host's
+ *     KIND_ID (1-12) plus appended ids 13-21. Generated from the host's
  *     RunnerSpec table (hexlib_amd/exec/genentry.py).
  *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
  *     stop/close/hwinfo) that validates a batch blob on the host, resolves
@@ -195,6 +195,13 @@ void matmul_epilogue_f16w_fp16(const hexlib_hf *a, const hexlib_hf *w,
 void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *wt,
                                 const float *bias, hexlib_hf *out,
                                 int M, int K, int N, int act);
+/* fp16(resid + fp16(act(a @ w + bias))), w given transposed as in
+ * matmul_epilogue_f16wt_fp16 (KIND 21): a linear followed by the residual
+ * add_fp16 that consumes it, each rounded as the reference stores it.
+ * resid [M, N] fp16 must not overlap a or wt. bias may be NULL. */
+void matmul_epilogue_f16wt_res_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
+                                    const hexlib_hf *resid, hexlib_hf *out,
+                                    int M, int K, int N, int act);
 /* act(a @ deq(w) + bias), w = q4_0 blocks of 32 along K of W^T [N, K] --
  * llama.cpp's native Linear layout (KIND 15). bias may be NULL. */
 void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
@@ -240,6 +247,7 @@ int matmul_epilogue_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16w_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q4k_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_f16wt_res_fp16_entry(const hexlib_args *a);
 int attention_fp16_entry(const hexlib_args *a);
 int attention_qk_v_fp16_entry(const hexlib_args *a);
 int rope_2d_qk_fp16_entry(const hexlib_args *a);

@@ -74,9 +74,15 @@ def matmul(arrays, attrs):  # structural.py:55-61
 def matmul_epilogue(arrays, attrs):  # fused.py:44-53
     out = (arrays[0] @ arrays[1] + arrays[2]).astype(arrays[0].dtype)
     act = attrs.get("act", "none")
-    if act == "none":
-        return (out,)
-    return REFERENCES[act]((out,), {})
+    if act != "none":
+        (out,) = REFERENCES[act]((out,), {})
+    if len(arrays) == 4:
+        # residual folded in (build extension): the linear's result is stored
+        # at `round` first, then add (elementwise.py:40-48)
+        if attrs.get("round") == "fp16":
+            out = out.astype(np.float16).astype(out.dtype)
+        out = (arrays[3] + out).astype(out.dtype)
+    return (out,)
 
 
 _NUMPY = {"fp32": np.float32, "fp16": np.float32, "int32": np.int32, "q4_0": np.float32}

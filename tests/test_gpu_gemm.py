@@ -217,3 +217,51 @@ def test_override_rejects_bad_values(dev):
     for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 3), (256, 256, 0, 0)]:
         assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
     assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 768, 0), (256, 3072, 768, 0), (8192, 3072, 768, 0),
+                                        (300, 320, 136, 1), (17, 64, 40, 2), (256, 768, 3072, 1)])
+def test_matmul_epilogue_f16wt_res(dev, M, Kd, N, act):
+    """KIND 21: the linear then the residual add in one epilogue. Bit-identical
+    to this library's own matmul_epilogue_f16wt followed by add_fp16 (same
+    tile plan, same accumulation order), including split-K shapes; and
+    within the harness tolerance of the oracle."""
+    r = rng(13)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    res = h16(r.standard_normal((M, N)))
+    da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+    dev.lib.matmul_epilogue_f16wt_res_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr), dev.ptr(d2),
+                                           M, Kd, N, act)
+    dev.check()
+    lin, got = dev.down(d1), dev.down(d2)
+    np.testing.assert_array_equal(got.view(np.uint16), K.add_fp16(res, lin).view(np.uint16))
+    want = K.add_fp16(res, K.matmul_epilogue_f16w(a, w, bias, act))
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("tile,splits,path", [((64, 64), 4, 2), ((128, 128), 3, 1), ((64, 64), 1, 1)])
+def test_residual_epilogue_every_path(dev, tile, splits, path):
+    """Residual epilogue through each code path the override can force:
+    direct-to-LDS and register-staged kernels, direct and split-K (reduce
+    kernel) epilogues, ragged M and N."""
+    r = rng(14)
+    M, Kd, N = 200, 1024, 200
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    res = h16(r.standard_normal((M, N)))
+    da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(tile[0], tile[1], splits, path) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, 0)
+        dev.lib.matmul_epilogue_f16wt_res_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr),
+                                               dev.ptr(d2), M, Kd, N, 0)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, dev.down(d1)).view(np.uint16))

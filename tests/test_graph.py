@@ -204,3 +204,30 @@ def test_fused_qkv_feeds_compute_the_reference_function():
     want = eager.run_fp32(fuse(g), feeds)[g.outputs[0]]
     got = eager.run_fp32(fuse(gq), E.fuse_qkv_feeds(feeds, cfg))[gq.outputs[0]]
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_fuse_residual():
+    """Each block's two residual adds fold into the fp16 linear feeding them;
+    the pos_embed add (const operand) and q4_0 linears do not; on the
+    storage-rounding oracle the result is unchanged bit for bit."""
+    from dataclasses import replace as _replace
+    from hexlib_amd.graph.fuse import fuse_residual
+    from oracle import eager
+    cfg = E.TINY_ENCODER
+    g = E.build_vision_encoder(cfg)
+    f = fuse(g)
+    r = fuse_residual(f)
+    assert len(f.ops) - len(r.ops) == 2 * cfg.depth
+    assert sum(1 for o in r.ops if o.kind == "matmul_epilogue" and len(o.inputs) == 4) == 2 * cfg.depth
+    assert sum(1 for o in r.ops if o.kind == "add") == 1
+    feeds = E.synthetic_feeds(g, cfg, seed=5)
+    a = eager.run_stored(f, feeds)[g.outputs[0]]
+    b = eager.run_stored(r, feeds)[g.outputs[0]]
+    np.testing.assert_array_equal(a, b)
+    q4 = fuse(E.build_vision_encoder(_replace(E.TINY_ENCODER, weight_dtype="q4_0")))
+    assert fuse_residual(q4) is q4
+    cfgq = _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
+    gq = E.build_vision_encoder(cfgq)
+    wb = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), residual=True)
+    assert wb.n_ops == 259 - 12 * 11 - 24
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_f16wt_res") == 24
