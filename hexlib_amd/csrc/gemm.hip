@@ -65,14 +65,18 @@ struct GemmArgs {
     long long ldr;
 };
 
+__device__ __forceinline__ bool hx_aligned8(const void *p) {
+    return (reinterpret_cast<uintptr_t>(p) & 7) == 0;
+}
+
 // One output's epilogue: act(acc + bias) rounded to fp16 and, with a residual
 // r, fp16(float(r) + float(that)) -- matmul_epilogue then add_fp16, each
 // rounded as the reference stores it (the sum is materialised in fp32 first,
 // so the compiler cannot fuse it into the fp16 conversion).
-__device__ __forceinline__ f16 epi(float v, int act, const f16 *r) {
+__device__ __forceinline__ f16 epi(float v, int act, bool has_r, f16 r) {
     const f16 h = (f16) apply_act(v, act);
-    if (!r) return h;
-    return (f16) f32_rounded((float) *r + (float) h);
+    if (!has_r) return h;
+    return (f16) f32_rounded((float) r + (float) h);
 }
 
 __device__ __forceinline__ f16 q4_val(float d, int q) { return (f16) (d * (float) (q - 8)); }
@@ -339,7 +343,8 @@ struct Gemm {
         }
 
         f16 *C = p.C + (long long) bz * p.sC;
-        const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C);
+        const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) &&
+                               (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -354,24 +359,21 @@ struct Gemm {
                     if (m >= p.M) continue;
                     f16 *dst = C + (long long) m * p.ldc + n;
                     if (vec_store && n + 3 < p.N) {
+                        const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
                         f16x4 o;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
+                        for (int e = 0; e < 4; ++e) o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R, r4[e]);
                         *reinterpret_cast<f16x4 *>(dst) = o;
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             if (n + e < p.N)
-                                dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
+                                dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R,
+                                             p.R ? p.R[m * p.ldr + n + e] : (f16) 0);
                     }
                 }
             }
         }
-    }
-
-    static __device__ __forceinline__ bool hx_aligned8(const void *p) {
-        return (reinterpret_cast<uintptr_t>(p) & 7) == 0;
     }
 };
 
@@ -524,7 +526,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
         return;
     }
     f16 *C = p.C + (long long) bz * p.sC;
-    const bool vec_store = (p.ldc & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0;
+    const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -539,16 +541,17 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
                 if (m >= p.M) continue;
                 f16 *dst = C + (long long) m * p.ldc + n;
                 if (vec_store && n + 3 < p.N) {
+                    const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
                     f16x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
+                    for (int e = 0; e < 4; ++e) o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R, r4[e]);
                     *reinterpret_cast<f16x4 *>(dst) = o;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         if (n + e < p.N)
-                            dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R ? p.R + m * p.ldr + n + e : nullptr);
+                            dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R,
+                                         p.R ? p.R[m * p.ldr + n + e] : (f16) 0);
                 }
             }
         }
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(TPB) void splitk_reduce(const float *__restrict__ w
             const int m = (int) (o / N), n = (int) (o % N);
             const float b = bias ? bias[n] : 0.0f;
             C[(long long) bz * sC + (long long) m * ldc + n] =
-                epi(s[e] + b, act, R ? R + (long long) m * ldr + n : nullptr);
+                epi(s[e] + b, act, R, R ? R[(long long) m * ldr + n] : (f16) 0);
         }
     }
 }

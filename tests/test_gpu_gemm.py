@@ -238,9 +238,10 @@ def test_matmul_epilogue_f16wt_res(dev, M, Kd, N, act):
                                            M, Kd, N, act)
     dev.check()
     lin, got = dev.down(d1), dev.down(d2)
+    # the add is exact given the linear; the linear meets the GEMM tolerance
+    # (a tolerance on the sum would be meaningless where r + lin cancels)
     np.testing.assert_array_equal(got.view(np.uint16), K.add_fp16(res, lin).view(np.uint16))
-    want = K.add_fp16(res, K.matmul_epilogue_f16w(a, w, bias, act))
-    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+    assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
 
 
 @pytest.mark.parametrize("tile,splits,path", [((64, 64), 4, 2), ((128, 128), 3, 1), ((64, 64), 1, 1)])

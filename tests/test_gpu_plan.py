@@ -229,7 +229,8 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=4)
     cfg = replace(cfg_ref, attention=mode)
     fused_feeds = E.fuse_qkv_feeds(feeds, cfg) if mode == "fused_qkv_rope" else feeds
-    (out,), wb = _run_plan(session, cfg, fused_feeds, graph_mode=True, residual=residual)
+    (out,), wb = _run_plan(session, cfg, fused_feeds, graph_mode=True, residual=residual,
+                           weight_layout="auto" if residual else None)
     assert wb.n_ops == 259 - 12 * (8 if mode == "fused" else 11) - (24 if residual else 0)
     want = _oracle(cfg_ref, feeds)
     err = np.abs(out - want).max()
