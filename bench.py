@@ -83,15 +83,17 @@ def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
 
 # ---- plan helpers -------------------------------------------------------------------------
 
-def build_plan(cfg, seed=0, weight_layout="auto", residual=True):
+def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True):
     """The product plan: fusions on (`residual` folds residual adds into the
-    fp16 linears; the config's `attention` picks the attention form)."""
+    fp16 linears, `rope` the q/k rope into the fused q/k/v linear; the
+    config's `attention` picks the attention form)."""
     from hexlib_amd import encoder as E
     from hexlib_amd.exec.wholeplan import build_whole_plan_batch
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=seed)
     return g, feeds, build_whole_plan_batch(g, feeds, weight_layout=weight_layout,
-                                            residual=residual and cfg.attention != "unfused")
+                                            residual=residual and cfg.attention != "unfused",
+                                            rope=rope and cfg.attention == "fused_qkv_rope")
 
 
 def time_replays(plan, steps: int, warmup: int) -> float:

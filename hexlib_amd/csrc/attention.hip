@@ -244,3 +244,11 @@ extern "C" void attention_qk_v_fp16(const hexlib_hf *qk, const hexlib_hf *qkv, h
     const long long hd = (long long) H * D;
     launch(qk, qk + hd, 2 * hd, qkv + 2 * hd, 3 * hd, out, rows, H, D, batch, scale);
 }
+
+extern "C" void attention_qkv_fp16(const hexlib_hf *qkv, hexlib_hf *out, int rows, int H, int D, int batch,
+                                   float scale) {
+    if (!qkv || !out || !dims_ok(rows, H, D, batch)) return;
+    if (!hx::aligned(qkv, 16) || !hx::aligned(out, 16)) return;
+    const long long hd = (long long) H * D;
+    launch(qkv, qkv + hd, 3 * hd, qkv + 2 * hd, 3 * hd, out, rows, H, D, batch, scale);
+}

@@ -63,10 +63,53 @@ struct GemmArgs {
     float *ws;                  // split-K workspace [batch][splits][M][N] fp32
     const f16 *R;               // residual [M, N] (row stride ldr) added after rounding, or null
     long long ldr;
+    // rope on output columns [0, rope_cols) in heads of rope_d, or null; the tables are
+    // stored transposed, [rope_d, M], so the 32 rows of an MFMA output column read 32
+    // consecutive floats; the weight rows of each rope head are stored pair-interleaved
+    // (see rope_store4)
+    const float *rcos, *rsin;
+    int rope_cols, rope_d;
 };
 
 __device__ __forceinline__ bool hx_aligned8(const void *p) {
     return (reinterpret_cast<uintptr_t>(p) & 7) == 0;
+}
+
+// Rope in the epilogue (rope columns only). The weight rows of each rope head
+// are stored pair-interleaved: computed column 2i of a head is the head's
+// feature i and column 2i + 1 its feature i + D/2, so a lane's 4 consecutive
+// columns n .. n + 3 (n % 4 == 0, D % 4 == 0) hold the two rotation pairs
+// (i0, i0 + D/2) and (i0 + 1, i0 + 1 + D/2), i0 = (n % D) / 2. Each value is
+// first rounded to fp16 (the linear's stored output), rotated in fp32 with the
+// products and the sum rounded separately, rounded to fp16 again (rope_2d_fp16's
+// arithmetic, kernels/rope_2d_fp16/baseline.c), and stored de-interleaved at
+// features (i0, i0 + 1) and (i0 + D/2, i0 + 1 + D/2) of the head.
+struct RopeQuad {
+    int lo, hi;   // output features of pair i0 (lo, lo + 1 holds pair i0 + 1) and of its partners
+    int t;        // table column of pair i0
+};
+
+__device__ __forceinline__ RopeQuad rope_quad(int n, int rope_d) {
+    const int lc = n % rope_d, i0 = lc >> 1;
+    return {n - lc + i0, n - lc + i0 + (rope_d >> 1), i0};
+}
+
+// c0 = cos[t], cos[t + 1]; c1 = cos[t + D/2], cos[t + 1 + D/2]; s0, s1 likewise
+__device__ __forceinline__ void rope_store4(f16 *crow, RopeQuad q, const float v[4], float2 c0, float2 c1,
+                                            float2 s0, float2 s1) {
+#pragma clang fp contract(off)
+    f16x2 lo, hi;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float x0 = (float) (f16) v[2 * u], x1 = (float) (f16) v[2 * u + 1];
+        const float ca = u ? c0.y : c0.x, sa = u ? s0.y : s0.x;
+        const float cb = u ? c1.y : c1.x, sb = u ? s1.y : s1.x;
+        const float p0 = x0 * ca, q0 = x1 * sa, p1 = x1 * cb, q1 = x0 * sb;
+        lo[u] = (f16) f32_rounded(p0 - q0);
+        hi[u] = (f16) f32_rounded(p1 + q1);
+    }
+    *reinterpret_cast<f16x2 *>(crow + q.lo) = lo;
+    *reinterpret_cast<f16x2 *>(crow + q.hi) = hi;
 }
 
 // One output's epilogue: act(acc + bias) rounded to fp16 and, with a residual
@@ -78,6 +121,17 @@ __device__ __forceinline__ f16 epi(float v, int act, bool has_r, f16 r) {
     if (!has_r) return h;
     return (f16) f32_rounded((float) r + (float) h);
 }
+
+// The unvectorised store of up to 4 consecutive outputs (ragged N, unaligned
+// rows); out of line so the tiled kernels' unrolled epilogues stay small.
+__device__ __noinline__ void store_tail(f16 *dst, int cnt, int act, const f16 *r, float v0, float v1,
+                                        float v2, float v3) {
+    const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (e < cnt) dst[e] = epi(v[e], act, r, r ? r[e] : (f16) 0);
+}
+
 
 __device__ __forceinline__ f16 q4_val(float d, int q) { return (f16) (d * (float) (q - 8)); }
 
@@ -365,11 +419,9 @@ struct Gemm {
                         for (int e = 0; e < 4; ++e) o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R, r4[e]);
                         *reinterpret_cast<f16x4 *>(dst) = o;
                     } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (n + e < p.N)
-                                dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R,
-                                             p.R ? p.R[m * p.ldr + n + e] : (f16) 0);
+                        store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr,
+                                   acc[j][i][g * 4] + bv[0], acc[j][i][g * 4 + 1] + bv[1],
+                                   acc[j][i][g * 4 + 2] + bv[2], acc[j][i][g * 4 + 3] + bv[3]);
                     }
                 }
             }
@@ -396,14 +448,15 @@ constexpr int DS_ROW = 64;  // halves per LDS row (128 B)
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
-template <int ROWS>
+template <int ROWS, int NW>
 __device__ __forceinline__ void lds_copy_slice(const f16 *__restrict__ base, long long ld, int row0,
                                                int rows_valid, int k0, f16 *lds) {
-    // ROWS x 64 halves: ROWS/8 wave-instructions, dealt round-robin to the 4 waves.
+    // ROWS x 64 halves: ROWS/8 wave-instructions, dealt round-robin to the NW waves.
+    static_assert(ROWS % (8 * NW) == 0, "slice rows must split evenly over the waves");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < ROWS / 32; ++j) {
-        const int rg = j * 4 + wave;                 // 8-row group
+    for (int j = 0; j < ROWS / (8 * NW); ++j) {
+        const int rg = j * NW + wave;                // 8-row group
         const int r = rg * 8 + (lane >> 3);          // row within the slice
         const int slot = lane & 7;
         const int c = slot ^ swz(r);
@@ -424,10 +477,12 @@ __device__ __forceinline__ void lds_copy_slice(const f16 *__restrict__ base, lon
 // s_waitcnt encoding (gfx9): vmcnt in [3:0] and [15:14]; expcnt/lgkmcnt left at max.
 #define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 
-template <int BM, int BN, int STAGES>
-__global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
-    constexpr int TM = BM / 64, TN = BN / 64;
-    constexpr int LOADS = BM / 32 + BN / 32;     // wave-instructions per slice per wave
+// WM x WN waves; each owns a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles.
+template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
+    constexpr int NW = WM * WN;
+    constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
+    constexpr int LOADS = (BM + BN) / (8 * NW);   // wave-instructions per slice per wave
     static_assert(STAGES >= 2 && LOADS * (STAGES - 2) <= 63, "vmcnt holds at most 63");
     __shared__ __attribute__((aligned(16))) f16 sA[STAGES][BM * DS_ROW];
     __shared__ __attribute__((aligned(16))) f16 sB[STAGES][BN * DS_ROW];
@@ -438,7 +493,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
     const f16 *B = reinterpret_cast<const f16 *>(p.B) + (long long) bz * p.sB;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+    const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
     const int kbeg = split * p.k_per_split;
     const int kend = min(p.K, kbeg + p.k_per_split);
     const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;   // K range is a multiple of 64
@@ -452,8 +507,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
     auto issue = [&](int kt, int st) {
         f16 *a = sA[st];
         f16 *b = sB[st];
-        lds_copy_slice<BM>(A, p.lda, m0, p.M, kbeg + kt * BK, a);
-        lds_copy_slice<BN>(B, p.ldb, n0, p.N, kbeg + kt * BK, b);
+        lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kbeg + kt * BK, a);
+        lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kbeg + kt * BK, b);
     };
 
 #pragma unroll
@@ -526,6 +581,73 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
         return;
     }
     f16 *C = p.C + (long long) bz * p.sC;
+    if constexpr (ROPE) {
+        // the rope entry point guarantees N % 4 == 0, rope_d % 4 == 0, ldc == N,
+        // an 8-byte aligned C, one batch and no residual: every group
+        // of 4 columns is in range as a whole and lies in one head or wholly past
+        // the rope heads. The bias and table loads of GB groups are issued before
+        // the first of their rotations, so their latencies overlap.
+        const int half = p.rope_d >> 1;
+        // column groups per load batch: 4 for one row block; 1 for more, which keeps
+        // the 128x128 tile under 192 VGPRs and so at 2 waves per SIMD
+        constexpr int GB = TM == 1 ? 4 : 1;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+#pragma unroll
+            for (int gb = 0; gb < 4; gb += GB) {
+                RopeQuad q[GB];
+                bool rope[GB];
+                float bv[GB][4];
+                float2 c0[GB][TM], c1[GB][TM], s0[GB][TM], s1[GB][TM];
+#pragma unroll
+                for (int h = 0; h < GB; ++h) {
+                    const int n = n0 + wn + j * 32 + (gb + h) * 8 + (lane >> 5) * 4;
+                    rope[h] = n < p.rope_cols;
+                    q[h] = rope[h] ? rope_quad(n, p.rope_d) : RopeQuad{n, n + 1, 0};
+                    const int f[4] = {q[h].lo, rope[h] ? q[h].hi : n + 1, q[h].lo + (rope[h] ? 1 : 2),
+                                      rope[h] ? q[h].hi + 1 : n + 3};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) bv[h][e] = (p.bias && n < p.N) ? p.bias[f[e]] : 0.0f;
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const int m = min(m0 + wm + i * 32 + (lane & 31), p.M - 1);
+                        if (rope[h]) {
+                            const long long ld = p.M, o = (long long) q[h].t * ld + m, oh = o + half * ld;
+                            c0[h][i] = float2{p.rcos[o], p.rcos[o + ld]};
+                            c1[h][i] = float2{p.rcos[oh], p.rcos[oh + ld]};
+                            s0[h][i] = float2{p.rsin[o], p.rsin[o + ld]};
+                            s1[h][i] = float2{p.rsin[oh], p.rsin[oh + ld]};
+                        }
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < GB; ++h) {
+                    const int g = gb + h;
+                    const int n = n0 + wn + j * 32 + g * 8 + (lane >> 5) * 4;
+                    if (n >= p.N) continue;
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const int m = m0 + wm + i * 32 + (lane & 31);
+                        if (m >= p.M) continue;
+                        f16 *crow = C + (long long) m * p.ldc;
+                        if (rope[h]) {
+                            float v[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = apply_act(acc[j][i][g * 4 + e] + bv[h][e], p.act);
+                            rope_store4(crow, q[h], v, c0[h][i], c1[h][i], s0[h][i], s1[h][i]);
+                        } else {
+                            f16x4 o;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                o[e] = epi(acc[j][i][g * 4 + e] + bv[h][e], p.act, false, (f16) 0);
+                            *reinterpret_cast<f16x4 *>(crow + n) = o;
+                        }
+                    }
+                }
+            }
+        }
+        return;
+    }
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -547,13 +669,115 @@ __global__ __launch_bounds__(TPB) void gemm_nk_lds(GemmArgs p) {
                     for (int e = 0; e < 4; ++e) o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R, r4[e]);
                     *reinterpret_cast<f16x4 *>(dst) = o;
                 } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < p.N)
-                            dst[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R,
-                                         p.R ? p.R[m * p.ldr + n + e] : (f16) 0);
+                    store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr,
+                               acc[j][i][g * 4] + bv[0], acc[j][i][g * 4 + 1] + bv[1],
+                               acc[j][i][g * 4 + 2] + bv[2], acc[j][i][g * 4 + 3] + bv[3]);
                 }
             }
+        }
+    }
+}
+
+// ---- W^T small-M path: register operands, K split across the waves -------------
+//
+// For small M (the encoder at batch 1: M = 256) the tiled kernels leave most
+// CUs idle and each wave's single accumulator makes its MFMAs a dependent
+// chain. Here a 256-thread workgroup owns a (32 TM) x (32 TN) output tile and
+// its 4 waves split K: wave w takes 64-wide K slices w, w + 4, ... Each lane loads
+// its MFMA operands straight from global memory (16 bytes = 8 consecutive k of
+// one row, exactly the v_mfma_f32_32x32x16_f16 operand), the next slice's
+// loads issued before the current slice is multiplied; no LDS staging and no
+// barrier in the loop. The waves' fp32 partial tiles are summed through LDS in
+// wave order 0..3 (fixed, so results are identical run to run), then bias,
+// activation, rounding and the optional residual are applied as in the other
+// epilogues. Requires K % 64 == 0 and 16-byte aligned rows.
+template <int TM, int TN>
+struct SkinnySlice {
+    f16x8 a[TM][4];    // activation rows 32 i + l % 32, k = 16 st + 8 (l / 32) .. +8
+    f16x8 b[TN][4];    // weight rows 32 j + l % 32
+};
+
+template <int TM, int TN>
+__global__ __launch_bounds__(TPB) void gemm_nk_skinny(GemmArgs p) {
+    constexpr int BM = 32 * TM, BN = 32 * TN;
+    __shared__ float part[4][BM][BN + 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, r = lane & 31;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int KT = p.K / BK;
+    const f16 *A = p.A;
+    const f16 *B = reinterpret_cast<const f16 *>(p.B);
+    // rows past M / N are loaded from a clamped (valid) row and never stored
+    const f16 *arow[TM];
+    const f16 *brow[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) arow[i] = A + (long long) min(m0 + 32 * i + r, p.M - 1) * p.lda + 8 * hl;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) brow[j] = B + (long long) min(n0 + 32 * j + r, p.N - 1) * p.ldb + 8 * hl;
+
+    auto load = [&](int kt, SkinnySlice<TM, TN> &sl) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) sl.a[i][st] = *reinterpret_cast<const f16x8 *>(arow[i] + k0 + 16 * st);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) sl.b[j][st] = *reinterpret_cast<const f16x8 *>(brow[j] + k0 + 16 * st);
+        }
+    };
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
+    SkinnySlice<TM, TN> cur, nxt;
+    int kt = wave;
+    if (kt < KT) load(kt, cur);
+    for (; kt < KT; kt += 4) {
+        if (kt + 4 < KT) load(kt + 4, nxt);
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.b[j][st], cur.a[i][st], acc[j][i], 0, 0, 0);
+        cur = nxt;
+    }
+
+    // acc[j][i][e] = partial C[m0 + 32 i + r][n0 + 32 j + (e/4)*8 + 4 hl + e%4]
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                part[wave][32 * i + r][32 * j + (e >> 2) * 8 + 4 * hl + (e & 3)] = acc[j][i][e];
+    __syncthreads();
+
+    // BM rows x BN columns, 4 consecutive columns per thread
+    const bool vec = (p.ldc & 3) == 0 && hx_aligned8(p.C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
+    for (int e = threadIdx.x; e < BM * (BN / 4); e += TPB) {
+        const int row = e / (BN / 4), c0 = (e % (BN / 4)) * 4;
+        const int m = m0 + row, n = n0 + c0;
+        if (m >= p.M || n >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            v[q] = ((part[0][row][c0 + q] + part[1][row][c0 + q]) + part[2][row][c0 + q]) + part[3][row][c0 + q];
+        f16 *dst = p.C + (long long) m * p.ldc + n;
+        if (vec && n + 3 < p.N) {
+            const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + (long long) m * p.ldr + n) : f16x4{};
+            f16x4 o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = epi(v[q] + (p.bias ? p.bias[n + q] : 0.0f), p.act, p.R, r4[q]);
+            *reinterpret_cast<f16x4 *>(dst) = o;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (n + q < p.N)
+                    dst[q] = epi(v[q] + (p.bias ? p.bias[n + q] : 0.0f), p.act, p.R,
+                                 p.R ? p.R[(long long) m * p.ldr + n + q] : (f16) 0);
         }
     }
 }
@@ -603,6 +827,51 @@ __global__ __launch_bounds__(TPB) void splitk_reduce(const float *__restrict__ w
     }
 }
 
+// splitk_reduce for the rope epilogue (N % 4 == 0, rope_d % 4 == 0, one batch,
+// no residual, tables [rope_d, M]): the same fixed-order sum, then each 4-column group of a rope
+// head is rotated and stored de-interleaved as the tiled kernel's rope
+// epilogue does (rope_store4); groups past the rope heads are stored plainly.
+__global__ __launch_bounds__(TPB) void splitk_reduce_rope(const float *__restrict__ ws,
+                                                          const float *__restrict__ bias,
+                                                          f16 *__restrict__ C, int M, int N, int splits,
+                                                          int act, const float *__restrict__ rcos,
+                                                          const float *__restrict__ rsin, int rope_cols,
+                                                          int rope_d) {
+    const long long per = (long long) M * N;
+    const long long quads = per / 4;
+    const long long stride = (long long) gridDim.x * TPB;
+    for (long long q = (long long) blockIdx.x * TPB + threadIdx.x; q < quads; q += stride) {
+        const long long idx = q * 4;
+        f32x4 v[MAX_SPLITS];
+#pragma unroll
+        for (int sp = 0; sp < MAX_SPLITS; ++sp)
+            if (sp < splits) v[sp] = *reinterpret_cast<const f32x4 *>(ws + sp * per + idx);
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sp = 0; sp < MAX_SPLITS; ++sp)
+            if (sp < splits) {
+                s[0] += v[sp][0]; s[1] += v[sp][1]; s[2] += v[sp][2]; s[3] += v[sp][3];
+            }
+        const int m = (int) (idx / N), n = (int) (idx % N);
+        f16 *crow = C + (long long) m * N;
+        if (n < rope_cols) {
+            const RopeQuad r = rope_quad(n, rope_d);
+            const int f[4] = {r.lo, r.hi, r.lo + 1, r.hi + 1};
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = apply_act(s[e] + (bias ? bias[f[e]] : 0.0f), act);
+            const long long ld = M, t = (long long) r.t * ld + m, th = t + (rope_d >> 1) * ld;
+            rope_store4(crow, r, o, float2{rcos[t], rcos[t + ld]}, float2{rcos[th], rcos[th + ld]},
+                        float2{rsin[t], rsin[t + ld]}, float2{rsin[th], rsin[th + ld]});
+        } else {
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = epi(s[e] + (bias ? bias[n + e] : 0.0f), act, false, (f16) 0);
+            *reinterpret_cast<f16x4 *>(crow + n) = o;
+        }
+    }
+}
+
 // ---- host side ------------------------------------------------------------------
 
 struct Tile {
@@ -642,17 +911,19 @@ float *workspace(size_t bytes) {
     return static_cast<float *>(p);
 }
 
-// Chooses the tile and split count. Cost = (rounds of workgroups over the 256
-// CUs) x (tile area / per-tile efficiency) x (K slices per split + a per-tile
-// pipeline fill), plus a fixed cost for the reduction launch when K is split.
-// Split-K only while the split grid still fits in one round. The constants
-// come from a sweep of every tile, split and path over the encoder's GEMM
-// shapes on MI355X (within 4% of the best configuration on average).
+// Chooses the tile and split count. Cost = (rounds of workgroups over the
+// 256 CUs x 2 resident workgroups each -- both tiles' kernels run at 2 waves
+// per SIMD) x (tile area / per-tile efficiency) x (K slices per split + a
+// per-tile pipeline fill), plus a fixed cost for the reduction launch when K
+// is split. Split-K only while the split grid still fits in one round. The
+// constants come from a sweep of every tile, split and path over the
+// encoder's GEMM shapes on MI355X (within 1% of the best configuration on
+// average).
 void plan_tiles(long long M, long long N, long long K, int batch, Tile &t, int &splits) {
     struct Cand { Tile t; double eff, fill; };
-    static const Cand cands[] = {{{128, 128}, 1.0, 10.0}, {{64, 64}, 0.25, 0.0}};
-    constexpr int CUS = 256;
-    constexpr double SPLIT_COST = 40000.0;   // the reduction kernel, in the same units
+    static const Cand cands[] = {{{128, 128}, 1.0, 20.0}, {{64, 64}, 0.2, 0.0}};
+    constexpr int SLOTS = 256 * 2;
+    constexpr double SPLIT_COST = 20000.0;   // the reduction kernel, in the same units
     constexpr int MIN_SPLIT_SLICES = 8;      // shorter K ranges are latency-bound: no gain
     const long long kt = (K + BK - 1) / BK;
     double best = 1e300;
@@ -661,10 +932,10 @@ void plan_tiles(long long M, long long N, long long K, int batch, Tile &t, int &
     for (const Cand &c : cands) {
         const long long tiles = ((M + c.t.bm - 1) / c.t.bm) * ((N + c.t.bn - 1) / c.t.bn) * batch;
         for (int s = 1; s <= MAX_SPLITS; s *= 2) {
-            if (s > 1 && (kt / s < MIN_SPLIT_SLICES || tiles * s > CUS)) break;
+            if (s > 1 && (kt / s < MIN_SPLIT_SLICES || tiles * s > SLOTS)) break;
             const long long per = (kt + s - 1) / s;
             const long long ss = (kt + per - 1) / per;
-            const long long rounds = (tiles * ss + CUS - 1) / CUS;
+            const long long rounds = (tiles * ss + SLOTS - 1) / SLOTS;
             const double area = (double) c.t.bm * c.t.bn;
             const double cost = (double) rounds * area * ((double) per + c.fill) / c.eff +
                                 (ss > 1 ? SPLIT_COST : 0.0);
@@ -691,16 +962,50 @@ void launch_tile(const GemmArgs &p, int batch, bool avec, bool bvec) {
 // replaces the heuristic's choice for every later GEMM in the process.
 std::atomic<int> g_ov_bm{0}, g_ov_bn{0}, g_ov_splits{0}, g_ov_path{0};
 
+// The small-M kernel trades data reuse for no LDS staging and no barriers: it
+// wins only where the whole GEMM is a few K slices over few columns (a sweep
+// of the encoder's shapes on MI355X: 256x768x768 5.7 us vs 7.9 us tiled; wider
+// N or longer K are faster tiled).
+bool skinny_auto(int M, int N, int K) { return M <= 256 && N <= 1024 && K <= 1024; }
+
+// The rope epilogue on the direct-to-LDS kernel, one split. It is its own
+// instantiation, so it costs the plain kernels no registers; there is no
+// 256x128 rope form (its 32 unrolled rope stores push the accumulators to
+// scratch), that tile runs as 128x128.
+void launch_lds_rope(const GemmArgs &p, Tile t) {
+    if (t.bm >= 128) t = {128, 128};
+    const dim3 grid((unsigned) ((p.N + t.bn - 1) / t.bn), (unsigned) ((p.M + t.bm - 1) / t.bm), 1);
+    if (t.bm == 128) HX_LAUNCH((gemm_nk_lds<128, 128, 2, 2, 2, true>), grid, dim3(TPB), 0, p);
+    else if (t.bm == 32) HX_LAUNCH((gemm_nk_lds<32, 64, 4, 1, 2, true>), grid, dim3(128), 0, p);
+    else if (t.bn == 32) HX_LAUNCH((gemm_nk_lds<64, 32, 4, 2, 1, true>), grid, dim3(128), 0, p);
+    else HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, true>), grid, dim3(TPB), 0, p);
+}
+
 template <int MODE>
 void launch(GemmArgs p, int batch, bool avec, bool bvec) {
+    const int path = g_ov_path.load();
+    p.splits = 1;
+    p.k_per_split = p.K;
+    p.ws = nullptr;
+    // small M: the register-operand kernel (K split across its waves, no split-K launch)
+    const bool skinny_ok = MODE == B_NK && batch == 1 && p.K % BK == 0 && p.lda % 8 == 0 &&
+                           p.ldb % 8 == 0 && avec && bvec && (p.M + 31) / 32 <= 65535 && !p.rcos;
+    if (skinny_ok && (path == 3 || (path == 0 && skinny_auto(p.M, p.N, p.K)))) {
+        int bm = g_ov_bm.load(), bn = g_ov_bn.load();
+        if (path != 3 || bm == 0) bm = bn = 32;
+        const dim3 grid((unsigned) ((p.N + bn - 1) / bn), (unsigned) ((p.M + bm - 1) / bm));
+        if (bm == 32 && bn == 32) HX_LAUNCH((gemm_nk_skinny<1, 1>), grid, dim3(TPB), 0, p);
+        else if (bm == 32) HX_LAUNCH((gemm_nk_skinny<1, 2>), grid, dim3(TPB), 0, p);
+        else if (bn == 32) HX_LAUNCH((gemm_nk_skinny<2, 1>), grid, dim3(TPB), 0, p);
+        else HX_LAUNCH((gemm_nk_skinny<2, 2>), grid, dim3(TPB), 0, p);
+        return;
+    }
     Tile t;
     int splits;
     plan_tiles(p.M, p.N, p.K, batch, t, splits);
     if (const int bm = g_ov_bm.load()) t = {bm, g_ov_bn.load()};
+    if (t.bm == 32 && t.bn == 32) t = {64, 64};   // the skinny-only tile, on a shape it cannot take
     if (const int s = g_ov_splits.load()) splits = s;
-    p.splits = 1;
-    p.k_per_split = p.K;
-    p.ws = nullptr;
     if (splits > 1) {
         const int kt = (p.K + BK - 1) / BK;
         const int per = (kt + splits - 1) / splits;
@@ -716,22 +1021,33 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     }
     bool lds_direct = MODE == B_NK && p.K % BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                       avec && bvec && p.k_per_split % BK == 0;
-    if (g_ov_path.load() == 1) lds_direct = false;
-    if (lds_direct) {
+    if (path == 1 && !p.rcos) lds_direct = false;   // the rope epilogue exists on this kernel only
+    if (p.rcos && !lds_direct) return;                 // unreachable: the rope entry point checks its preconditions
+    if (lds_direct && p.rcos && p.splits == 1) {
+        launch_lds_rope(p, t);
+    } else if (lds_direct) {
         dim3 grid((unsigned) ((p.N + t.bn - 1) / t.bn), (unsigned) ((p.M + t.bm - 1) / t.bm),
                   (unsigned) (batch * p.splits));
         if (t.bm == 256) HX_LAUNCH((gemm_nk_lds<256, 128, 3>), grid, dim3(TPB), 0, p);
         else if (t.bm == 128) HX_LAUNCH((gemm_nk_lds<128, 128, 2>), grid, dim3(TPB), 0, p);
+        else if (t.bm == 32) HX_LAUNCH((gemm_nk_lds<32, 64, 4, 1, 2>), grid, dim3(128), 0, p);
+        else if (t.bn == 32) HX_LAUNCH((gemm_nk_lds<64, 32, 4, 2, 1>), grid, dim3(128), 0, p);
         else HX_LAUNCH((gemm_nk_lds<64, 64, 4>), grid, dim3(TPB), 0, p);
-    } else if (t.bm == 256) launch_tile<256, 128, MODE>(p, batch, avec, bvec);
+    } else if (t.bm < 64 || t.bn < 64) launch_tile<64, 64, MODE>(p, batch, avec, bvec);
+    else if (t.bm == 256) launch_tile<256, 128, MODE>(p, batch, avec, bvec);
     else if (t.bm == 128) launch_tile<128, 128, MODE>(p, batch, avec, bvec);
     else launch_tile<64, 64, MODE>(p, batch, avec, bvec);
-    if (p.splits > 1) {
+    if (p.splits > 1 && p.rcos) {
+        HX_LAUNCH(splitk_reduce_rope, dim3(hx::blocks_for((long long) p.M * p.N / 4, TPB, 4096)), dim3(TPB), 0,
+                  (const float *) p.ws, p.bias, p.C, p.M, p.N, p.splits, p.act, p.rcos, p.rsin, p.rope_cols,
+                  p.rope_d);
+    } else if (p.splits > 1) {
         const long long quads = ((long long) p.M * p.N + 3) / 4 * batch;
         HX_LAUNCH(splitk_reduce, dim3(hx::blocks_for(quads, TPB, 4096)), dim3(TPB), 0,
                   (const float *) p.ws, p.bias, p.C, p.ldc, p.sC, p.M, p.N, p.splits, p.act, batch, p.R, p.ldr);
     }
 }
+
 
 bool dims_ok(int M, int K, int N, int batch) {
     return M > 0 && K > 0 && N > 0 && batch > 0 && batch <= 65535 && (M + 63) / 64 <= 65535;
@@ -777,8 +1093,10 @@ int prepare_workspace() {
 
 extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
     const bool tile_ok = (bm == 0 && bn == 0) || (bm == 256 && bn == 128) ||
-                         (bm == 128 && bn == 128) || (bm == 64 && bn == 64);
-    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 2) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+                         (bm == 128 && bn == 128) || (bm == 64 && bn == 64) ||
+                         (bm == 32 && bn == 64) || (bm == 64 && bn == 32) ||
+                         (path == 3 && bm == 32 && bn == 32);
+    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 3) return HEXLIB_DSP_ERR_INVAL_PARAMS;
     g_ov_bm = bm;
     g_ov_bn = bn;
     g_ov_splits = splits;
@@ -816,6 +1134,23 @@ extern "C" void matmul_epilogue_f16wt_res_fp16(const hexlib_hf *a, const hexlib_
     p.R = reinterpret_cast<const f16 *>(resid);
     p.ldr = N;
     launch<B_NK>(p, 1, K % 8 == 0 && hx::aligned(a, 16), K % 8 == 0 && hx::aligned(wt, 16));
+}
+
+extern "C" void matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
+                                                const float *costab, const float *sintab, hexlib_hf *out,
+                                                int M, int K, int N, int act, int rope_heads, int rope_dim) {
+    if (!a || !wt || !out || !costab || !sintab || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
+    const long long rope_cols = 2LL * rope_heads * rope_dim;
+    // the direct-to-LDS kernel's preconditions (its epilogue implements the rope)
+    if (rope_heads <= 0 || rope_dim <= 0 || rope_dim % 4 || rope_cols > N || N % 4 || K % BK || K % 8 ||
+        !hx::aligned(a, 16) || !hx::aligned(wt, 16) || !hx::aligned(out, 8))
+        return;
+    GemmArgs p = args(a, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act);
+    p.rcos = costab;
+    p.rsin = sintab;
+    p.rope_cols = (int) rope_cols;
+    p.rope_d = rope_dim;
+    launch<B_NK>(p, 1, true, true);
 }
 
 extern "C" void matmul_epilogue_fp16(const hexlib_hf *a, const unsigned char *w, const float *bias,

@@ -27,7 +27,7 @@ import numpy as np
 from hexlib_amd import lib as _lib
 from hexlib_amd.exec import wire
 from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, select
-from hexlib_amd.exec.wholeplan import ALIGN, WholePlanBatch, align_up, decode
+from hexlib_amd.exec.wholeplan import ALIGN, WholePlanBatch, align_up, decode, stage_col_major_rope
 from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
 
 
@@ -204,7 +204,10 @@ class GpuBackend:
             else:
                 arr = np.ascontiguousarray(a, dtype=np.float16 if dt == "fp16" else np.float32)
                 shape = arr.shape
-                data = (np.ascontiguousarray(arr.T) if lays[i] == "col_major" else arr).tobytes()
+                if lays[i] == "col_major_rope":
+                    data = stage_col_major_rope(arr, int(attrs["rope_heads"]), int(attrs["rope_dim"]))
+                else:
+                    data = (np.ascontiguousarray(arr.T) if lays[i] == "col_major" else arr).tobytes()
             off = len(payload)
             tensors.append(wire.TensorDesc(0, off, len(data), dt, lays[i], wire.pad_ne(shape)))
             shapes.append(tuple(shape))

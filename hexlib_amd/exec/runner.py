@@ -50,6 +50,8 @@ KIND_ID: dict[str, int] = {
     "attention_qk_v": 19,
     "rope_2d_qk": 20,
     "matmul_epilogue_f16wt_res": 21,
+    "matmul_epilogue_f16wt_rope": 22,
+    "attention_qkv": 23,
 }
 
 
@@ -285,6 +287,28 @@ SPECS: dict[str, RunnerSpec] = {
         weight=(1, "fp16"), primary=False, rank=2,
         notes="extension: a linear with the residual add that consumes it folded into the "
               "epilogue (fused by hexlib_amd.graph.fuse.fuse_residual); fp16 W^T only"),
+    "matmul_epilogue_f16wt_rope": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_f16wt_rope_fp16", ("fp16", "fp16", "fp32", "fp32", "fp32"), "fp16",
+        _MM_SCALARS + (_S("attr:rope_heads", "rope_heads"), _S("attr:rope_dim", "rope_dim")),
+        layouts=("row_major", "col_major_rope", "row_major", "col_major", "col_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*rope_dim", "(uint64_t)M*rope_dim",
+                 "(uint64_t)M*N"),
+        checks=("K % 64 == 0", "N % 4 == 0", "rope_dim % 4 == 0", "2LL * rope_heads * rope_dim <= N",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
+                "((uintptr_t)a->buf[5] & 7) == 0"),
+        weight=(1, "fp16"), primary=False, rank=2,
+        notes="extension: the fused q/k/v linear with rope_2d on its q and k heads in the epilogue "
+              "(fused by hexlib_amd.graph.fuse.fuse_rope)"),
+    "attention_qkv": RunnerSpec(
+        "attention", "attention_qkv_fp16", ("fp16",), "fp16",
+        (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),
+         _S("attr:batch", "batch"), _S("attr:scale", "scale", "float")),
+        extents=("(uint64_t)rows*3*H*D", "(uint64_t)rows*H*D"),
+        checks=("a->ne[0][1] == 3", "D == 32 || D == 64", "rows % batch == 0",
+                "(uint64_t)batch * H <= 65535",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0"),
+        rank=4,
+        notes="extension: attention with q, k, v from one [rows, 3, H, D] tensor"),
     "attention_qk_v": RunnerSpec(
         "attention", "attention_qk_v_fp16", ("fp16", "fp16"), "fp16",
         (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),

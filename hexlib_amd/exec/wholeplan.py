@@ -32,7 +32,7 @@ import numpy as np
 
 from hexlib_amd.exec import wire
 from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, RunnerSpec, select
-from hexlib_amd.graph.fuse import fuse, fuse_residual
+from hexlib_amd.graph.fuse import fuse, fuse_residual, fuse_rope
 from hexlib_amd.graph.ir import Graph
 from hexlib_amd.graph.ir import nbytes as ir_nbytes
 from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
@@ -76,6 +76,20 @@ class WholePlanBatch:
     op_specs: tuple[str, ...] = field(default=())
     const_bytes: int = 0
     graph_ops: tuple = field(default=())   # the plan's non-reshape graph ops, in wire order
+
+
+def stage_col_major_rope(w, heads: int, d: int) -> bytes:
+    """A `[K, N]` fp16 weight in the `col_major_rope` layout: stored `[N, K]`
+    (W^T), with the rows of each of the first `2 * heads` heads of `d`
+    pair-interleaved -- stored row `h*d + 2i` is feature `h*d + i` and row
+    `h*d + 2i + 1` is feature `h*d + i + d/2` -- so a GEMM tile holds both
+    halves of every rotated pair in adjacent columns."""
+    wt = np.ascontiguousarray(np.asarray(w, dtype=np.float16).T)
+    i = np.arange(d)
+    src = np.where(i % 2 == 0, i // 2, i // 2 + d // 2)
+    rows = (np.arange(2 * heads)[:, None] * d + src[None, :]).reshape(-1)
+    wt[:2 * heads * d] = wt[rows]
+    return wt.tobytes()
 
 
 def _spec_for(op, graph: Graph, weight_layout: str | None) -> tuple[str, RunnerSpec]:
@@ -132,11 +146,15 @@ def _reuse_offsets(g: Graph, acts, reshape_src, owner, wbytes) -> tuple[dict[str
 
 def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                            weight_layout: str | None = "auto", fuse_first: bool = True,
-                           fd: int = 0, reuse: bool = True, residual: bool = False) -> WholePlanBatch:
+                           fd: int = 0, reuse: bool = True, residual: bool = False,
+                           rope: bool = False) -> WholePlanBatch:
     """`residual=True` also folds each residual add into the fp16 linear that
-    feeds it (`fuse_residual`), when fp16 weights are staged transposed (the
-    only layout with that kernel)."""
+    feeds it (`fuse_residual`), and `rope=True` the q/k rope of a fused q/k/v
+    projection into that linear (`fuse_rope`), when fp16 weights are staged
+    transposed (the only layout with those kernels)."""
     g = fuse(graph) if fuse_first else graph
+    if rope and weight_layout in ("auto", "col_major"):
+        g = fuse_rope(g)
     if residual and weight_layout in ("auto", "col_major"):
         g = fuse_residual(g)
     tensors = g.tensors
@@ -169,11 +187,15 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
             raise WholePlanError(f"{name!r} is used as {prev!r} and {value!r} ({where})")
 
     op_specs: dict[int, tuple[str, RunnerSpec]] = {}
+    rope_of: dict[str, tuple[int, int]] = {}    # col_major_rope weight -> (heads, head_dim)
     for op in g.ops:
         if op.kind == "reshape":
             continue
         name, spec = _spec_for(op, g, weight_layout)
         op_specs[op.id] = (name, spec)
+        if "col_major_rope" in spec.buf_layouts():
+            claim(rope_of, op.inputs[1], (int(op.attrs["rope_heads"]), int(op.attrs["rope_dim"])),
+                  f"op {op.id} rope")
         lays = spec.buf_layouts()
         for i, n in enumerate(op.inputs):
             claim(layout_of, n, lays[i], f"op {op.id} src{i}")
@@ -239,6 +261,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                 data = pack_q4_0_kgrouped(np.asarray(value))
             else:
                 data = pack_q4_0_nblocked(np.asarray(value))
+        elif p.layout == "col_major_rope":
+            data = stage_col_major_rope(value, *rope_of[n])
         elif p.layout == "col_major":
             data = np.ascontiguousarray(np.asarray(value, dtype=_NP[p.dtype]).T).tobytes()
         else:

@@ -114,3 +114,51 @@ def fuse_residual(graph: Graph) -> Graph:
     ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
     tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
     return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)
+
+
+def fuse_rope(graph: Graph) -> Graph:
+    readers: dict[str, list[Op]] = {}
+    producer: dict[str, Op] = {}
+    for op in graph.ops:
+        for name in op.inputs:
+            readers.setdefault(name, []).append(op)
+        for name in op.outputs:
+            producer[name] = op
+    outputs = set(graph.outputs)
+    replaced: dict[int, Op] = {}
+    absorbed: set[int] = set()
+    dropped: set[str] = set()
+    for rope in graph.ops:
+        if rope.kind != "rope_2d_qk":
+            continue
+        qkv4, cos, sin = rope.inputs
+        qk = rope.outputs[0]
+        shp = producer.get(qkv4)
+        if shp is None or shp.kind != "reshape" or qk in outputs:
+            continue
+        mm = producer.get(shp.inputs[0])
+        if mm is None or mm.kind != "matmul_epilogue" or len(mm.inputs) != 3:
+            continue
+        if graph.tensor(mm.inputs[1]).dtype != "fp16" or shp.inputs[0] in outputs:
+            continue
+        if len(readers.get(shp.inputs[0], [])) != 1 or len(readers.get(qk, [])) != 1:
+            continue
+        attn = readers[qk][0]
+        if attn.kind != "attention" or tuple(attn.inputs) != (qk, qkv4):
+            continue
+        if sorted(op.id for op in readers.get(qkv4, [])) != sorted((rope.id, attn.id)):
+            continue
+        _, _, heads, d = graph.tensor(qkv4).shape
+        replaced[mm.id] = Op(id=mm.id, kind="matmul_epilogue", inputs=tuple(mm.inputs) + (cos, sin),
+                             outputs=mm.outputs,
+                             attrs={**dict(mm.attrs), "round": graph.tensor(mm.outputs[0]).dtype,
+                                    "rope_heads": int(heads), "rope_dim": int(d)})
+        replaced[attn.id] = Op(id=attn.id, kind="attention", inputs=(qkv4,), outputs=attn.outputs,
+                               attrs=dict(attn.attrs))
+        absorbed.add(rope.id)
+        dropped.add(qk)
+    if not replaced:
+        return graph
+    ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
+    tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
+    return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)

@@ -58,6 +58,13 @@ def _matmul_epilogue_infer(inputs, attrs):
     bias = inputs[2]
     if bias.shape != (inputs[1].shape[-1],):
         raise ValueError(f"bias {bias.shape} != ({inputs[1].shape[-1]},)")
+    if len(inputs) == 4 and inputs[3].shape != out[0]:     # residual (build extension)
+        raise ValueError(f"residual {inputs[3].shape} != output {out[0]}")
+    if len(inputs) == 5:                                     # rope tables (build extension)
+        heads, d = int(attrs["rope_heads"]), int(attrs["rope_dim"])
+        rows = out[0][0]
+        if inputs[3].shape != (rows, d) or inputs[4].shape != (rows, d) or 2 * heads * d > out[0][-1]:
+            raise ValueError(f"rope tables {inputs[3].shape} for {heads} heads of {d} over {out[0]}")
     return (out,)
 
 
@@ -119,7 +126,12 @@ def _attention_infer(inputs, attrs):
     head_dim], qkv [rows, 3, heads, head_dim]): q, k from the first, v from
     the third slot of the second. Output [rows, heads, head_dim]."""
     batch = int(attrs.get("batch", 1))
-    if len(inputs) == 2:
+    if len(inputs) == 1:
+        (qkv,) = inputs
+        if len(qkv.shape) != 4 or qkv.shape[1] != 3:
+            raise ValueError(f"attention over one tensor wants [rows, 3, heads, head_dim], got {qkv.shape}")
+        out = (qkv.shape[0], qkv.shape[2], qkv.shape[3])
+    elif len(inputs) == 2:
         qk, qkv = inputs
         rows, two, heads, d = qk.shape if len(qk.shape) == 4 else (0, 0, 0, 0)
         if two != 2 or qkv.shape != (rows, 3, heads, d):

@@ -9,7 +9,7 @@
  *     dimensions make the call a silent no-op, as in the reference.
  *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
  *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
- *     KIND_ID (1-12) plus appended ids 13-21. Generated from the host's
+ *     KIND_ID (1-12) plus appended ids 13-23. Generated from the host's
  *     RunnerSpec table (hexlib_amd/exec/genentry.py).
  *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
  *     stop/close/hwinfo) that validates a batch blob on the host, resolves
@@ -66,13 +66,16 @@ enum hexlib_dsp_status {
     HEXLIB_DSP_ERR_CACHE = 15
 };
 
-/* Layout ids: hexlib_dsp.h:168-170, plus 3 = q4_0 grouped along K of W^T
- * and 4 = a [K, N] weight stored transposed ([N, K], K contiguous). */
+/* Layout ids: hexlib_dsp.h:168-170, plus 3 = q4_0 grouped along K of W^T,
+ * 4 = a [K, N] weight stored transposed ([N, K], K contiguous) and 5 = layout
+ * 4 with the rows of each rope head pair-interleaved (row 2i of a head holds
+ * feature i, row 2i + 1 feature i + D/2). */
 #define HEXLIB_LAYOUT_ROW_MAJOR     0u
 #define HEXLIB_LAYOUT_TILED_32X32   1u
 #define HEXLIB_LAYOUT_Q4_0_REPACKED 2u
 #define HEXLIB_LAYOUT_Q4_0_KGROUP   3u
 #define HEXLIB_LAYOUT_COL_MAJOR     4u
+#define HEXLIB_LAYOUT_COL_MAJOR_ROPE 5u
 
 /* Dtype ids: hexlib/runtime/wire.py:61. */
 #define HEXLIB_DTYPE_FP32  0u
@@ -195,6 +198,19 @@ void matmul_epilogue_f16w_fp16(const hexlib_hf *a, const hexlib_hf *w,
 void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *wt,
                                 const float *bias, hexlib_hf *out,
                                 int M, int K, int N, int act);
+/* A linear whose output columns [0, 2 * rope_heads * rope_dim) are rotated by
+ * rope_2d_fp16's split-half rope in heads of rope_dim (KIND 22): the q and k
+ * slots of a fused q/k/v projection. out = act(a @ w + bias) rounded to fp16,
+ * then each rope head rotated with fp32 tables cos/sin and rounded again --
+ * bit-identical to matmul_epilogue_f16wt_fp16 followed by rope_2d_qk_fp16.
+ * wt is W^T [N, K] with the rows of each rope head pair-interleaved (layout
+ * 5); bias is in feature order; cos and sin are rope_2d_fp16's [M, rope_dim]
+ * tables stored transposed, [rope_dim, M] (layout 4). Requires K % 64 == 0,
+ * N % 4 == 0, rope_dim % 4 == 0, 16-byte aligned a and wt, 8-byte aligned
+ * out; else a no-op. */
+void matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
+                                     const float *costab, const float *sintab, hexlib_hf *out,
+                                     int M, int K, int N, int act, int rope_heads, int rope_dim);
 /* fp16(resid + fp16(act(a @ w + bias))), w given transposed as in
  * matmul_epilogue_f16wt_fp16 (KIND 21): a linear followed by the residual
  * add_fp16 that consumes it, each rounded as the reference stores it.
@@ -229,6 +245,10 @@ void rope_2d_qk_fp16(const hexlib_hf *qkv, const float *costab, const float *sin
  * 16-byte aligned. */
 void attention_qk_v_fp16(const hexlib_hf *qk, const hexlib_hf *qkv, hexlib_hf *out,
                          int rows, int H, int D, int batch, float scale);
+/* attention_fp16 with q, k and v all taken from one [rows, 3, H, D] tensor
+ * (KIND 23): the output of matmul_epilogue_f16wt_rope_fp16. */
+void attention_qkv_fp16(const hexlib_hf *qkv, hexlib_hf *out, int rows, int H, int D, int batch,
+                        float scale);
 
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
@@ -248,6 +268,8 @@ int matmul_epilogue_f16w_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q4k_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_f16wt_res_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_f16wt_rope_fp16_entry(const hexlib_args *a);
+int attention_qkv_fp16_entry(const hexlib_args *a);
 int attention_fp16_entry(const hexlib_args *a);
 int attention_qk_v_fp16_entry(const hexlib_args *a);
 int rope_2d_qk_fp16_entry(const hexlib_args *a);
@@ -264,10 +286,11 @@ int   hexlib_gpu_take_error(void);
 const char *hexlib_gpu_error_string(int hip_error);
 const char *hexlib_gpu_status_name(int status);
 /* GEMM tuning override for every later GEMM launch in the process: tile
- * bm x bn (256x128, 128x128, 64x64; 0x0 = heuristic), split-K count
+ * bm x bn (256x128, 128x128, 64x64, 32x64, 64x32; 0x0 = heuristic), split-K count
  * (0 = heuristic, at most 16) and W^T code path (0 = automatic,
- * 1 = register-staged, 2 = direct-to-LDS where its preconditions hold).
- * Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
+ * 1 = register-staged, 2 = direct-to-LDS, 3 = the small-M register-operand
+ * kernel with tile 32x32 or 32x64; 2 and 3 apply where their preconditions
+ * hold). Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
 int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path);
 /* sizeof of each wire struct, in declaration order above (batch_hdr, buf_desc,
  * tensor, op_desc, rsp_hdr, op_result, hexlib_args); returns the count. */

@@ -26,6 +26,7 @@ any summation order the GPU picks.
 | attention_fp16       | hexlib/models/vit.py:185-193 chain, fused         | equals the composition of the registry references; uniform / one-hot closed forms |
 | rope_2d_qk_fp16      | rope_2d_fp16 on the q, k slots of a fused qkv     | rope_2d_fp16 (pinned bit-exact) per slot |
 | attention_qk_v_fp16  | attention_fp16 on strided q, k, v                 | attention_fp16 |
+| permute_rope_rows    | the col_major_rope weight layout (row order only) | per-head halves land on even / odd rows; v rows untouched |
 """
 from __future__ import annotations
 
@@ -175,3 +176,15 @@ def attention_qk_v_fp16(qk, qkv, batch, scale):
     """attention_fp16 with q, k from qk [rows, 2, H, D] and v from qkv [rows, 3, H, D]."""
     qk, qkv = np.asarray(qk, np.float16), np.asarray(qkv, np.float16)
     return attention_fp16(qk[:, 0], qk[:, 1], qkv[:, 2], batch, scale)
+
+
+def permute_rope_rows(wt, heads, d):
+    """W^T [N, K] with the rows of each of the first 2*heads heads of d
+    pair-interleaved (row 2i = feature i, row 2i + 1 = feature i + d/2):
+    the col_major_rope layout."""
+    wt = np.asarray(wt).copy()
+    idx = np.arange(d)
+    src = np.where(idx % 2 == 0, idx // 2, idx // 2 + d // 2)
+    for h in range(2 * heads):
+        wt[h * d:(h + 1) * d] = wt[h * d + src]
+    return wt

@@ -82,6 +82,17 @@ def matmul_epilogue(arrays, attrs):  # fused.py:44-53
         if attrs.get("round") == "fp16":
             out = out.astype(np.float16).astype(out.dtype)
         out = (arrays[3] + out).astype(out.dtype)
+    if len(arrays) == 5:
+        # rope folded in (build extension): the linear's result is stored at
+        # `round`, then rope_2d (structural.py:240-254) on its first
+        # 2 * rope_heads heads of rope_dim -- the q and k slots
+        if attrs.get("round") == "fp16":
+            out = out.astype(np.float16).astype(out.dtype)
+        heads, d = int(attrs["rope_heads"]), int(attrs["rope_dim"])
+        rows = out.shape[0]
+        qk = out[:, :2 * heads * d].reshape(rows, 2 * heads, d)
+        (rot,) = rope_2d((qk, arrays[3], arrays[4]), {})
+        out = np.concatenate([rot.reshape(rows, -1), out[:, 2 * heads * d:]], axis=1).astype(out.dtype)
     return (out,)
 
 
@@ -133,6 +144,9 @@ def attention(arrays, attrs):
     if len(arrays) == 2:   # (qk [rows, 2, H, D], qkv [rows, 3, H, D])
         qk, qkv = arrays
         arrays = (qk[:, 0], qk[:, 1], qkv[:, 2])
+    elif len(arrays) == 1:  # (qkv [rows, 3, H, D])
+        (qkv,) = arrays
+        arrays = (qkv[:, 0], qkv[:, 1], qkv[:, 2])
     q, k, v = (np.asarray(a, np.float64) for a in arrays)
     batch = int(attrs.get("batch", 1))
     rows, heads, d = q.shape

@@ -106,3 +106,25 @@ def test_rope_2d_qk_and_attention_qk_v(dev, B, T, H, D):
     want = K.attention_qk_v_fp16(qk, qkv, B, D ** -0.5)
     report(f"attention_qk_v B{B} T{T} H{H} D{D}", got, want)
     assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (2, 33, 2, 64), (3, 17, 2, 32)])
+def test_attention_qkv(dev, B, T, H, D):
+    """KIND 23: q, k, v all read from one [rows, 3, H, D] tensor -- the output
+    of the q/k/v linear with rope in its epilogue. Bit-identical to KIND 19 fed
+    the same q, k slots as a separate [rows, 2, H, D] tensor (same kernel,
+    other strides), and within tolerance of the oracle."""
+    r = np.random.default_rng(90 + T)
+    rows = B * T
+    qkv = h16(r.standard_normal((rows, 3, H, D)))
+    qk = np.ascontiguousarray(qkv[:, :2])
+    dqkv, dqk = dev.up(qkv), dev.up(qk)
+    o1, o2 = dev.empty((rows, H, D), np.float16), dev.empty((rows, H, D), np.float16)
+    dev.lib.attention_qkv_fp16(dev.ptr(dqkv), dev.ptr(o1), rows, H, D, B, D ** -0.5)
+    dev.lib.attention_qk_v_fp16(dev.ptr(dqk), dev.ptr(dqkv), dev.ptr(o2), rows, H, D, B, D ** -0.5)
+    dev.check()
+    got = dev.down(o1)
+    np.testing.assert_array_equal(got.view(np.uint16), dev.down(o2).view(np.uint16))
+    want = K.attention_fp16(qkv[:, 0], qkv[:, 1], qkv[:, 2], B, D ** -0.5)
+    report(f"attention_qkv B{B} T{T} H{H} D{D}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()

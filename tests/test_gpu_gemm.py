@@ -168,7 +168,7 @@ def test_split_k_is_deterministic(dev, fn):
 
 
 @pytest.mark.parametrize("M,Kd,N", [(256, 768, 768), (300, 320, 138), (33, 1024, 70), (8, 4096, 256)])
-@pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 128)])
+@pytest.mark.parametrize("tile", [(64, 64), (128, 128), (256, 128), (32, 64), (64, 32)])
 @pytest.mark.parametrize("splits", [2, 5, 16])
 @pytest.mark.parametrize("path", [1, 2])
 def test_forced_tiles_and_splits(dev, M, Kd, N, tile, splits, path):
@@ -214,7 +214,8 @@ def test_forced_split_batched_matmul(dev, splits):
 
 
 def test_override_rejects_bad_values(dev):
-    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 3), (256, 256, 0, 0)]:
+    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 4), (256, 256, 0, 0),
+                 (32, 128, 0, 3), (128, 32, 0, 3)]:
         assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
     assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
 
@@ -266,3 +267,105 @@ def test_residual_epilogue_every_path(dev, tile, splits, path):
     finally:
         dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
     np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, dev.down(d1)).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,Kd,N", [(256, 768, 768), (256, 3072, 768), (256, 768, 2304), (64, 3072, 1024),
+                                    (300, 320, 136), (1, 896, 4864), (33, 64, 40), (512, 256, 96)])
+@pytest.mark.parametrize("bm,bn", [(32, 32), (32, 64), (64, 32), (64, 64)])
+@pytest.mark.parametrize("residual", [False, True])
+def test_skinny_small_m_path(dev, M, Kd, N, bm, bn, residual):
+    """The small-M register-operand kernel (path 3), both tile widths, ragged
+    M and N, K from one to 48 slices, with and without the residual epilogue:
+    against the oracle, and bit-identical on a repeat call."""
+    r = rng(15)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    res = h16(r.standard_normal((M, N)))
+    da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
+    outs = []
+    assert dev.lib.hexlib_gpu_gemm_override(bm, bn, 0, 3) == 1
+    try:
+        for _ in range(2):
+            do = dev.empty((M, N), np.float16)
+            if residual:
+                dev.lib.matmul_epilogue_f16wt_res_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr),
+                                                       dev.ptr(do), M, Kd, N, 1)
+            else:
+                dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, 1)
+            dev.check()
+            outs.append(dev.down(do))
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    np.testing.assert_array_equal(outs[1].view(np.uint16), outs[0].view(np.uint16))
+    lin = K.matmul_epilogue_f16w(a, w, bias, 1)
+    if residual:
+        # the add is exact on the fp16 linear; compare the linear part through it
+        got_lin = (outs[0].astype(np.float32) - res.astype(np.float32))
+        assert np.abs(got_lin - lin.astype(np.float32)).max() <= 2e-2
+    else:
+        assert K.close_f16(outs[0], lin, 1e-2, 1e-3).all()
+
+
+def _rope_tables(r, M, d):
+    ang = r.random((M, d // 2)) * 6.0
+    return (np.concatenate([np.cos(ang)] * 2, axis=1).astype(np.float32),
+            np.concatenate([np.sin(ang)] * 2, axis=1).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,Kd,heads,d,extra,tile,splits", [
+    (256, 768, 12, 64, 768, None, 1), (1024, 768, 12, 64, 768, None, 1), (65, 128, 2, 32, 64, None, 1),
+    (200, 256, 3, 16, 0, None, 1), (256, 768, 12, 64, 768, (64, 64), 1), (256, 768, 12, 64, 768, (128, 128), 1),
+    (300, 512, 4, 64, 256, (256, 128), 1), (130, 256, 2, 64, 128, (32, 64), 1), (130, 256, 2, 64, 128, (64, 32), 1),
+    (256, 768, 12, 64, 768, (64, 64), 2), (200, 1024, 3, 16, 32, (64, 64), 3), (300, 512, 4, 64, 256, (128, 128), 4),
+    (256, 768, 12, 64, 768, None, 0)])
+def test_matmul_epilogue_f16wt_rope(dev, M, Kd, heads, d, extra, tile, splits):
+    """KIND 22: the fused q/k/v linear with rope_2d on its first 2 * heads
+    heads in the epilogue, its weight in the pair-interleaved col_major_rope
+    layout: in the tiled kernel's epilogue (one split) or in the split-K
+    reduce. Bit-identical to this library's direct-to-LDS matmul_epilogue_f16wt
+    with the same tile and split count followed by rope_2d on those heads; and
+    the linear part within the harness tolerance of the oracle. splits 0 is
+    the heuristic plan (the encoder's shape: tiles too few to fill the chip, so
+    it splits K)."""
+    r = rng(21)
+    N = 2 * heads * d + extra
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    cos, sin = _rope_tables(r, M, d)
+    da, db = dev.up(a), dev.up(bias)
+    dc, ds = dev.up(np.ascontiguousarray(cos.T)), dev.up(np.ascontiguousarray(sin.T))   # [d, M]
+    dw = dev.up(np.ascontiguousarray(w.T))
+    dwr = dev.up(K.permute_rope_rows(w.T, heads, d))
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    bm, bn = tile or (0, 0)
+    assert dev.lib.hexlib_gpu_gemm_override(bm, bn, splits, 2) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, 0)
+        dev.lib.matmul_epilogue_f16wt_rope_fp16(dev.ptr(da), dev.ptr(dwr), dev.ptr(db), dev.ptr(dc), dev.ptr(ds),
+                                                dev.ptr(d2), M, Kd, N, 0, heads, d)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    lin, got = dev.down(d1), dev.down(d2)
+    qk = lin[:, :2 * heads * d].reshape(M, 2 * heads, d)
+    want = lin.copy()
+    want[:, :2 * heads * d] = K.rope_2d_fp16(qk, cos, sin).reshape(M, -1)
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+    assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, 0), 1e-2, 1e-3).all()
+
+
+def test_matmul_epilogue_f16wt_rope_invalid_is_a_silent_no_op(dev):
+    """Shapes the rope epilogue has no form for leave the output untouched."""
+    M, Kd, heads, d = 64, 128, 2, 32
+    N = 3 * heads * d
+    z = np.zeros((M, Kd), np.float16)
+    da, dw = dev.up(z), dev.up(np.zeros((N, Kd), np.float16))
+    db, dc = dev.up(np.zeros(N, np.float32)), dev.up(np.zeros((d, M), np.float32))
+    out = dev.up(np.full((M, N), 7, np.float16))
+    for kk, hh, dd in ((96, heads, d), (Kd, heads, 30), (Kd, 4, d)):
+        dev.lib.matmul_epilogue_f16wt_rope_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dc), dev.ptr(dc),
+                                                dev.ptr(out), M, kk, N, 0, hh, dd)
+    dev.check()
+    assert (dev.down(out) == 7).all()

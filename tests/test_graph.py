@@ -231,3 +231,44 @@ def test_fuse_residual():
     wb = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), residual=True)
     assert wb.n_ops == 259 - 12 * 11 - 24
     assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_f16wt_res") == 24
+
+
+def test_fuse_rope():
+    """The q/k rope of each block folds into its fused q/k/v linear and the
+    attention reads q, k, v from the linear's output; on the storage-rounding
+    oracle the encoder output is unchanged bit for bit. Only the fused-QKV
+    graph form has the pattern."""
+    from dataclasses import replace as _replace
+    from hexlib_amd.graph.fuse import fuse_rope
+    from oracle import eager
+    cfg = _replace(E.TINY_ENCODER, attention="fused_qkv_rope")
+    g = E.build_vision_encoder(cfg)
+    f = fuse(g)
+    r = fuse_rope(f)
+    assert len(f.ops) - len(r.ops) == cfg.depth
+    assert not any(o.kind == "rope_2d_qk" for o in r.ops)
+    assert sum(1 for o in r.ops if o.kind == "matmul_epilogue" and len(o.inputs) == 5) == cfg.depth
+    assert sum(1 for o in r.ops if o.kind == "attention" and len(o.inputs) == 1) == cfg.depth
+    feeds = E.fuse_qkv_feeds(E.synthetic_feeds(E.build_vision_encoder(E.TINY_ENCODER), E.TINY_ENCODER,
+                                               seed=6), cfg)
+    a = eager.run_stored(f, feeds)[g.outputs[0]]
+    b = eager.run_stored(r, feeds)[g.outputs[0]]
+    np.testing.assert_array_equal(a, b)
+    for other in ("unfused", "fused"):
+        fo = fuse(E.build_vision_encoder(_replace(E.TINY_ENCODER, attention=other)))
+        assert fuse_rope(fo) is fo
+    cfgq = _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
+    gq = E.build_vision_encoder(cfgq)
+    wb = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), residual=True, rope=True)
+    assert wb.n_ops == 259 - 12 * 11 - 24 - 12
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_f16wt_rope") == 12
+    assert sum(1 for s in wb.op_specs if s == "attention_qkv") == 12
+    assert KIND_ID_OF("matmul_epilogue_f16wt_rope") == 22 and KIND_ID_OF("attention_qkv") == 23
+    # rope needs the transposed fp16 weight layout: with another one nothing folds
+    wb2 = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), weight_layout=None, rope=True)
+    assert wb2.n_ops == 259 - 12 * 11
+
+
+def KIND_ID_OF(name):
+    from hexlib_amd.exec.runner import KIND_ID
+    return KIND_ID[name]

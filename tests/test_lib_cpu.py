@@ -278,3 +278,61 @@ def test_attention_qk_v_entry_checks(sess, two, three, D, want):
     blob = wire.pack_batch([wire.BufDesc(3, int(offs[3]))], t, [op])
     assert sess.mmap(3, int(offs[3])) == OK
     assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+def _blob(kind, tensors, params, n_src):
+    """One op over tensors laid out back to back at 256-byte steps."""
+    offs, descs, cur = [], [], 0
+    for shape, dt, lay in tensors:
+        n = int(np.prod(shape)) * (2 if dt == "fp16" else 4)
+        descs.append(wire.TensorDesc(0, cur, n, dt, lay, wire.pad_ne(shape)))
+        cur += (n + 255) // 256 * 256
+    op = wire.OpDesc(KIND_ID[kind], params, tuple(range(n_src)), (n_src,))
+    return wire.pack_batch([wire.BufDesc(3, cur)], descs, [op]), cur
+
+
+@pytest.mark.parametrize("M,K,N,heads,d,table_layout,want", [
+    (256, 768, 2304, 12, 64, "col_major", "OK"), (65, 128, 192, 2, 32, "col_major", "OK"),
+    (64, 64, 128, 2, 32, "col_major", "OK"),
+    (64, 96, 192, 2, 32, "col_major", "ERR_INVAL_PARAMS"),    # K not a multiple of 64
+    (64, 128, 192, 2, 30, "col_major", "ERR_INVAL_PARAMS"),   # rope_dim not a multiple of 4
+    (64, 128, 192, 4, 32, "col_major", "ERR_INVAL_PARAMS"),   # 2 * heads * rope_dim > N
+    (64, 128, 192, 2, 32, "row_major", "ERR_REQUIRES")])      # tables not stored transposed
+def test_matmul_epilogue_rope_entry_checks(sess, M, K, N, heads, d, table_layout, want):
+    blob, size = _blob("matmul_epilogue_f16wt_rope",
+                       [((M, K), "fp16", "row_major"), ((K, N), "fp16", "col_major_rope"),
+                        ((N,), "fp32", "row_major"), ((M, d), "fp32", table_layout),
+                        ((M, d), "fp32", "col_major"), ((M, N), "fp16", "row_major")],
+                       (0, heads, d), 5)
+    assert sess.mmap(3, size) == OK
+    assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+@pytest.mark.parametrize("three,D,batch,want", [(3, 64, 1, "OK"), (3, 32, 2, "OK"), (2, 64, 1, "ERR_INVAL_PARAMS"),
+                                                (3, 48, 1, "ERR_INVAL_PARAMS"), (3, 64, 3, "ERR_INVAL_PARAMS")])
+def test_attention_qkv_entry_checks(sess, three, D, batch, want):
+    rows, H = 64, 2
+    blob, size = _blob("attention_qkv", [((rows, three, H, D), "fp16", "row_major"),
+                                         ((rows, H, D), "fp16", "row_major")],
+                       (batch, wire.float_param(D ** -0.5)), 1)
+    assert sess.mmap(3, size) == OK
+    assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+def test_col_major_rope_staging_matches_the_oracle_permutation():
+    """The product's staging of a col_major_rope weight against the oracle's
+    row-by-row restatement; rows past the 2 * heads rope heads (the v slot)
+    stay plain W^T, and the permutation is a bijection on each head."""
+    from hexlib_amd.exec.wholeplan import stage_col_major_rope
+    from oracle import kernels as K
+    r = np.random.default_rng(2)
+    for Kd, heads, d, N in ((64, 2, 32, 192), (128, 3, 8, 80), (64, 12, 64, 2304)):
+        w = r.standard_normal((Kd, N)).astype(np.float16)
+        got = np.frombuffer(stage_col_major_rope(w, heads, d), np.float16).reshape(N, Kd)
+        want = K.permute_rope_rows(w.T, heads, d)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(got[2 * heads * d:], w.T[2 * heads * d:])
+        for h in range(2 * heads):
+            blk = got[h * d:(h + 1) * d]
+            np.testing.assert_array_equal(blk[0::2], w.T[h * d:h * d + d // 2])
+            np.testing.assert_array_equal(blk[1::2], w.T[h * d + d // 2:(h + 1) * d])
