@@ -70,6 +70,10 @@ def op_work(spec_name: str, in_shapes, out_shape, in_dtypes, out_dtype) -> tuple
         m, k = in_shapes[0]
         n = in_shapes[1][-1]
         return "mfma", 2.0 * m * k * n
+    if spec_name.startswith("layernorm_matmul_epilogue"):   # (x, ln_w, ln_b, w, bias)
+        m, k = in_shapes[0]
+        n = in_shapes[3][-1]
+        return "mfma", 2.0 * m * k * n
     total = sum(nb(s, d) for s, d in zip(in_shapes, in_dtypes)) + nb(out_shape, out_dtype)
     return "hbm", float(total)
 
@@ -83,17 +87,22 @@ def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
 
 # ---- plan helpers -------------------------------------------------------------------------
 
-def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True):
+def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True, layernorm=False):
     """The product plan: fusions on (`residual` folds residual adds into the
     fp16 linears, `rope` the q/k rope into the fused q/k/v linear; the
-    config's `attention` picks the attention form)."""
+    config's `attention` picks the attention form). `layernorm` (folding a
+    LayerNorm into the linear it feeds) is off: every workgroup of that
+    kernel normalises its whole row block again, 48 times per row at fc1,
+    which costs more than the separate launch it saves (18.6 us against
+    9.4 + 2.5 us on MI355X)."""
     from hexlib_amd import encoder as E
     from hexlib_amd.exec.wholeplan import build_whole_plan_batch
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=seed)
     return g, feeds, build_whole_plan_batch(g, feeds, weight_layout=weight_layout,
                                             residual=residual and cfg.attention != "unfused",
-                                            rope=rope and cfg.attention == "fused_qkv_rope")
+                                            rope=rope and cfg.attention == "fused_qkv_rope",
+                                            layernorm=layernorm and cfg.attention != "unfused")
 
 
 def time_replays(plan, steps: int, warmup: int) -> float:
@@ -177,11 +186,12 @@ def per_op_in_plan(plan, g, reps: int = 40) -> list[dict]:
 def dominant_op(g, wb):
     """The plan's GEMM row with the most algorithmic work per image (launches
     x FLOPs; ties: first in plan order). For the cfg-4 encoder plan that is
-    the MLP up-projection fc1, 256x768x3072 (12 launches, tied with fc2 in
-    work; fc1 runs as one kernel, fc2 as split-K partials plus a reduction)."""
+    the MLP up-projection fc1, 256x768x3072 with its LayerNorm folded in (12
+    launches, tied with fc2 in work; fc1 runs as one kernel, fc2 as split-K
+    partials plus a reduction)."""
     rows = []
     for (spec, ins, out), (count, idx, _) in unique_ops(g, wb).items():
-        if not spec.startswith("matmul_epilogue"):
+        if not spec.startswith(("matmul_epilogue", "layernorm_matmul_epilogue")):
             continue
         flops = op_work(spec, [s for s, _ in ins], out[0], [d for _, d in ins], out[1])[1]
         rows.append((count * flops, -idx, spec, ins, out, count))

@@ -13,17 +13,38 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define HX_WAVE 64
 
-// Butterfly over all 64 lanes; every lane ends with the full result.
+// Lane exchange within a 16-lane row through a DPP operand modifier (a VALU
+// operand, no LDS round trip): 0xB1 / 0x4E swap lanes xor 1 / xor 2 within
+// each quad, 0x141 mirrors each half-row (lane i <-> 7 - i), 0x140 each row
+// (i <-> 15 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                                 false));
+}
+
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over all 64 lanes (all active); every lane ends with the same bits:
+// pairwise within quads, half-rows and rows (each step adds two equal-order
+// partial sums, so both partners compute the same value), then the four row
+// sums as (r0 + r1) + (r2 + r3).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, HX_WAVE);
-    return v;
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, HX_WAVE));
-    return v;
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
 // Returns v as an fp32 register value the backend cannot see through. Without

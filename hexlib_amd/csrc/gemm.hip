@@ -39,6 +39,7 @@
 #include <vector>
 
 #include "device.h"
+#include "lnmath.h"
 #include "internal.h"
 
 namespace {
@@ -69,6 +70,10 @@ struct GemmArgs {
     // (see rope_store4)
     const float *rcos, *rsin;
     int rope_cols, rope_d;
+    // LayerNorm of A's rows (over all K) applied before the product, or null:
+    // out = epilogue(LN(A) @ B), LN(A) rounded to fp16 as layernorm_fp16 stores it
+    const float *ln_w, *ln_b;
+    float ln_eps;
 };
 
 __device__ __forceinline__ bool hx_aligned8(const void *p) {
@@ -477,14 +482,80 @@ __device__ __forceinline__ void lds_copy_slice(const f16 *__restrict__ base, lon
 // s_waitcnt encoding (gfx9): vmcnt in [3:0] and [15:14]; expcnt/lgkmcnt left at max.
 #define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 
+// The LayerNorm prologue keeps A's whole row block resident in LDS: K <= 768.
+constexpr int LN_KT = 12;
+
+// Normalises the resident A row block in place: each wave takes BM / NW rows,
+// with layernorm_fp16's lane mapping (VEC 8, NCH chunks) and arithmetic, and
+// writes LN(x) rounded to fp16 back over x. Rows go in groups of RG: all of a
+// group's reads, then its RG independent reductions (their shuffle chains
+// overlap), then its writes. Rows past M hold a clamped copy of row M - 1 and
+// are normalised harmlessly.
+template <int BM, int NW, int NCH>
+__device__ __forceinline__ void ln_rows_in_lds(f16 (*sA)[BM * DS_ROW], const GemmArgs &p) {
+    constexpr int RG = 4;
+    static_assert((BM / NW) % RG == 0, "row groups must split the wave's rows");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float g[NCH][8], b[NCH][8];
+    bool ok[NCH];
+    int off[NCH];   // the chunk's slice and 16-byte column, before the row's swizzle
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        const int k0 = (ch * 64 + lane) * 8;
+        ok[ch] = k0 < p.K;
+        off[ch] = ok[ch] ? k0 : 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            g[ch][j] = ok[ch] ? p.ln_w[k0 + j] : 0.0f;
+            b[ch][j] = ok[ch] ? p.ln_b[k0 + j] : 0.0f;
+        }
+    }
+    for (int r0 = wave * (BM / NW); r0 < (wave + 1) * (BM / NW); r0 += RG) {
+        float v[RG][NCH][8];
+        f16 *at[RG][NCH];
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            const int r = r0 + q;
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) {
+                const int c = (off[ch] & 63) >> 3;
+                at[q][ch] = sA[off[ch] >> 6] + r * DS_ROW + ((c ^ swz(r)) << 3);
+                const f16x8 t = ok[ch] ? *reinterpret_cast<const f16x8 *>(at[q][ch]) : f16x8{};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[q][ch][j] = ok[ch] ? (float) t[j] : 0.0f;
+            }
+        }
+        float mean[RG], inv[RG];
+#pragma unroll
+        for (int q = 0; q < RG; ++q) ln_row_stats<8, NCH>(v[q], ok, p.K, p.ln_eps, mean[q], inv[q]);
+#pragma unroll
+        for (int q = 0; q < RG; ++q)
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) {
+                if (!ok[ch]) continue;
+                f16x8 t;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) t[j] = (f16) ln_apply(v[q][ch][j], inv[q], g[ch][j], b[ch][j]);
+                *reinterpret_cast<f16x8 *>(at[q][ch]) = t;
+            }
+    }
+}
+
+// lgkmcnt(0) with vmcnt and expcnt left at max: this wave's LDS writes are done.
+#define HX_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4))
+
 // WM x WN waves; each owns a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles.
-template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false>
+// LN: A's row block is loaded whole, layer-normalised in LDS, and only B
+// streams through the ring (BM = 64, K <= 64 * LN_KT, 512 <= K).
+template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false, bool LN = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     constexpr int NW = WM * WN;
     constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
-    constexpr int LOADS = (BM + BN) / (8 * NW);   // wave-instructions per slice per wave
+    // wave-instructions per ring slice per wave
+    constexpr int LOADS = (LN ? BN : BM + BN) / (8 * NW);
     static_assert(STAGES >= 2 && LOADS * (STAGES - 2) <= 63, "vmcnt holds at most 63");
-    __shared__ __attribute__((aligned(16))) f16 sA[STAGES][BM * DS_ROW];
+    static_assert(!LN || (BM / (8 * NW)) * LN_KT + LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(16))) f16 sA[LN ? LN_KT : STAGES][BM * DS_ROW];
     __shared__ __attribute__((aligned(16))) f16 sB[STAGES][BN * DS_ROW];
 
     const int bz = blockIdx.z / p.splits;
@@ -505,15 +576,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
         for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
 
     auto issue = [&](int kt, int st) {
-        f16 *a = sA[st];
-        f16 *b = sB[st];
-        lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kbeg + kt * BK, a);
-        lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kbeg + kt * BK, b);
+        if constexpr (!LN) lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kbeg + kt * BK, sA[st]);
+        lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kbeg + kt * BK, sB[st]);
     };
 
+    if constexpr (LN) {
+        // the whole A row block first, then the ring's first B slices; wait for
+        // A only, normalise it in place, and publish it before the main loop
+        for (int kt = 0; kt < KT; ++kt) lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kt * BK, sA[kt]);
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < KT) issue(s, s);
+        for (int s = 0; s < STAGES - 1; ++s)
+            if (s < KT) issue(s, s);
+        if (KT >= STAGES - 1) HX_WAIT_VMCNT(LOADS * (STAGES - 1));
+        else HX_WAIT_VMCNT(0);
+        __builtin_amdgcn_s_barrier();
+        if (p.K > 512) ln_rows_in_lds<BM, NW, 2>(sA, p);
+        else ln_rows_in_lds<BM, NW, 1>(sA, p);
+        HX_WAIT_LGKM0();
+        __builtin_amdgcn_s_barrier();
+    } else {
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s)
+            if (s < KT) issue(s, s);
+    }
 
     for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
 #pragma unroll
@@ -530,7 +615,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
             // LDS reads completed before the MFMAs that consumed them.
             __builtin_amdgcn_s_barrier();
             if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (st + STAGES - 1) % STAGES);
-            const f16 *as = sA[st];
+            const f16 *as = LN ? sA[kt] : sA[st];
             const f16 *bs = sB[st];
 #pragma unroll
             for (int ks = 0; ks < BK; ks += 16) {
@@ -981,6 +1066,13 @@ void launch_lds_rope(const GemmArgs &p, Tile t) {
     else HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, true>), grid, dim3(TPB), 0, p);
 }
 
+// The LayerNorm-prologue form: 64x64 tiles, one split (every workgroup reads
+// its whole A row block anyway).
+void launch_ln(const GemmArgs &p) {
+    const dim3 grid((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64), 1);
+    HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, false, true>), grid, dim3(TPB), 0, p);
+}
+
 template <int MODE>
 void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     const int path = g_ov_path.load();
@@ -1151,6 +1243,27 @@ extern "C" void matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *a, const hexlib
     p.rope_cols = (int) rope_cols;
     p.rope_d = rope_dim;
     launch<B_NK>(p, 1, true, true);
+}
+
+// LayerNorm over K then the W^T linear, in one launch. Preconditions of the
+// prologue: 512 <= K <= 64 * LN_KT, K % 64 == 0, 16-byte aligned x and wt.
+bool ln_ok(const hexlib_hf *x, const float *ln_w, const float *ln_b, const hexlib_hf *wt, int K) {
+    return x && ln_w && ln_b && wt && K >= 512 && K <= 64 * LN_KT && K % 64 == 0 && hx::aligned(x, 16) &&
+           hx::aligned(wt, 16);
+}
+
+extern "C" void layernorm_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const float *ln_w,
+                                                     const float *ln_b, const hexlib_hf *wt,
+                                                     const float *bias, hexlib_hf *out, int M, int K,
+                                                     int N, int act, float eps) {
+    if (!out || !dims_ok(M, K, N, 1) || act < 0 || act > 2 || !ln_ok(x, ln_w, ln_b, wt, K)) return;
+    GemmArgs p = args(x, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act);
+    p.splits = 1;
+    p.k_per_split = K;
+    p.ln_w = ln_w;
+    p.ln_b = ln_b;
+    p.ln_eps = eps;
+    launch_ln(p);
 }
 
 extern "C" void matmul_epilogue_fp16(const hexlib_hf *a, const unsigned char *w, const float *bias,

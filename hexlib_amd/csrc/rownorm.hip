@@ -13,6 +13,7 @@
 // x * (1/sqrt(mean(x^2) + eps)) * w (kernels/rmsnorm_fp16/kernel_api.h:9-12).
 #include "device.h"
 #include "internal.h"
+#include "lnmath.h"
 
 namespace {
 
@@ -105,23 +106,9 @@ __global__ __launch_bounds__(TPB) void layernorm_regs(const f16 *__restrict__ x,
     if (row >= R) return;
     RowRegs<VEC, NCH> r;
     r.load(x + row * C, C, lane, 0.0f);
-    float s = 0.0f;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) s += r.v[ch][j];
-    const float mean = wave_sum(s) / (float) C;
-    float q = 0.0f;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            const float d = r.ok[ch] ? r.v[ch][j] - mean : 0.0f;
-            r.v[ch][j] = d;
-            q += d * d;
-        }
-    const float inv = 1.0f / sqrtf(wave_sum(q) / (float) C + eps);
-    r.store(y + row * C, lane, [=](float d, int c) { return d * inv * w[c] + b[c]; });
+    float mean, inv;
+    ln_row_stats<VEC, NCH>(r.v, r.ok, C, eps, mean, inv);
+    r.store(y + row * C, lane, [=](float d, int c) { return ln_apply(d, inv, w[c], b[c]); });
 }
 
 template <int VEC, int NCH>

@@ -52,6 +52,7 @@ KIND_ID: dict[str, int] = {
     "matmul_epilogue_f16wt_res": 21,
     "matmul_epilogue_f16wt_rope": 22,
     "attention_qkv": 23,
+    "layernorm_matmul_epilogue_f16wt": 24,
 }
 
 
@@ -299,6 +300,18 @@ SPECS: dict[str, RunnerSpec] = {
         weight=(1, "fp16"), primary=False, rank=2,
         notes="extension: the fused q/k/v linear with rope_2d on its q and k heads in the epilogue "
               "(fused by hexlib_amd.graph.fuse.fuse_rope)"),
+    "layernorm_matmul_epilogue_f16wt": RunnerSpec(
+        "layernorm_matmul_epilogue", "layernorm_matmul_epilogue_f16wt_fp16",
+        ("fp16", "fp32", "fp32", "fp16", "fp32"), "fp16",
+        (_S("dim:0:0", "M"), _S("dim:0:1", "K"), _S("dim:3:1", "N"), _S("attr:act", "act", codes=_ACT_CODES),
+         _S("attr:eps", "eps", "float")),
+        layouts=("row_major", "row_major", "row_major", "col_major", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "K", "K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
+        checks=("K >= 512", "K <= 768", "K % 64 == 0",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[3] & 15) == 0"),
+        weight=(3, "fp16"), rank=2,
+        notes="extension: layernorm over K then the W^T linear, one launch "
+              "(fused by hexlib_amd.graph.fuse.fuse_layernorm)"),
     "attention_qkv": RunnerSpec(
         "attention", "attention_qkv_fp16", ("fp16",), "fp16",
         (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),

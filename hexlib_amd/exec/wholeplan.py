@@ -32,7 +32,7 @@ import numpy as np
 
 from hexlib_amd.exec import wire
 from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, RunnerSpec, select
-from hexlib_amd.graph.fuse import fuse, fuse_residual, fuse_rope
+from hexlib_amd.graph.fuse import fuse, fuse_layernorm, fuse_residual, fuse_rope
 from hexlib_amd.graph.ir import Graph
 from hexlib_amd.graph.ir import nbytes as ir_nbytes
 from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
@@ -147,16 +147,19 @@ def _reuse_offsets(g: Graph, acts, reshape_src, owner, wbytes) -> tuple[dict[str
 def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                            weight_layout: str | None = "auto", fuse_first: bool = True,
                            fd: int = 0, reuse: bool = True, residual: bool = False,
-                           rope: bool = False) -> WholePlanBatch:
+                           rope: bool = False, layernorm: bool = False) -> WholePlanBatch:
     """`residual=True` also folds each residual add into the fp16 linear that
-    feeds it (`fuse_residual`), and `rope=True` the q/k rope of a fused q/k/v
-    projection into that linear (`fuse_rope`), when fp16 weights are staged
-    transposed (the only layout with those kernels)."""
+    feeds it (`fuse_residual`), `rope=True` the q/k rope of a fused q/k/v
+    projection into that linear (`fuse_rope`) and `layernorm=True` each
+    LayerNorm into the linear it feeds (`fuse_layernorm`), when fp16 weights
+    are staged transposed (the only layout with those kernels)."""
     g = fuse(graph) if fuse_first else graph
     if rope and weight_layout in ("auto", "col_major"):
         g = fuse_rope(g)
     if residual and weight_layout in ("auto", "col_major"):
         g = fuse_residual(g)
+    if layernorm and weight_layout in ("auto", "col_major"):
+        g = fuse_layernorm(g)
     tensors = g.tensors
     io = set(g.inputs) | set(g.outputs)
     consts = {n for n, t in tensors.items() if t.const}
@@ -194,8 +197,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
         name, spec = _spec_for(op, g, weight_layout)
         op_specs[op.id] = (name, spec)
         if "col_major_rope" in spec.buf_layouts():
-            claim(rope_of, op.inputs[1], (int(op.attrs["rope_heads"]), int(op.attrs["rope_dim"])),
-                  f"op {op.id} rope")
+            claim(rope_of, op.inputs[spec.buf_layouts().index("col_major_rope")],
+                  (int(op.attrs["rope_heads"]), int(op.attrs["rope_dim"])), f"op {op.id} rope")
         lays = spec.buf_layouts()
         for i, n in enumerate(op.inputs):
             claim(layout_of, n, lays[i], f"op {op.id} src{i}")

@@ -8,6 +8,8 @@ adds (activation + activation) never fuse.
 """
 from __future__ import annotations
 
+import math
+
 from hexlib_amd.graph.ir import Graph, Op
 
 FUSABLE_ACTS = ("gelu_tanh", "gelu_erf")
@@ -157,6 +159,49 @@ def fuse_rope(graph: Graph) -> Graph:
                                attrs=dict(attn.attrs))
         absorbed.add(rope.id)
         dropped.add(qk)
+    if not replaced:
+        return graph
+    ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
+    tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
+    return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)
+
+
+def fuse_layernorm(graph: Graph, max_rows: int = 2048) -> Graph:
+    readers: dict[str, list[Op]] = {}
+    producer: dict[str, Op] = {}
+    for op in graph.ops:
+        for name in op.inputs:
+            readers.setdefault(name, []).append(op)
+        for name in op.outputs:
+            producer[name] = op
+    outputs = set(graph.outputs)
+    replaced: dict[int, Op] = {}
+    absorbed: set[int] = set()
+    dropped: set[str] = set()
+    for ln in graph.ops:
+        if ln.kind != "layernorm":
+            continue
+        y = ln.outputs[0]
+        users = readers.get(y, [])
+        if y in outputs or len(users) != 1:
+            continue
+        mm = users[0]
+        # the plain linear only: with the rope tables the fused op would have seven
+        # sources, one more than a wire op carries (hexlib/runtime/wire.py MAX_SRC)
+        if mm.kind != "matmul_epilogue" or len(mm.inputs) != 3 or mm.inputs[0] != y:
+            continue
+        if y in mm.inputs[1:] or graph.tensor(mm.inputs[1]).dtype != "fp16":
+            continue
+        x = graph.tensor(ln.inputs[0])
+        rows, feats = math.prod(x.shape[:-1]), x.shape[-1]
+        if len(x.shape) != 2 or not 512 <= feats <= 768 or feats % 64 or rows > max_rows:
+            continue
+        replaced[mm.id] = Op(id=mm.id, kind="layernorm_matmul_epilogue",
+                             inputs=tuple(ln.inputs) + tuple(mm.inputs[1:]), outputs=mm.outputs,
+                             attrs={**dict(mm.attrs), "eps": ln.attrs["eps"],
+                                    "ln_round": graph.tensor(y).dtype})
+        absorbed.add(ln.id)
+        dropped.add(y)
     if not replaced:
         return graph
     ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)

@@ -68,6 +68,14 @@ def _matmul_epilogue_infer(inputs, attrs):
     return (out,)
 
 
+def _ln_matmul_infer(inputs, attrs):
+    """(x, ln_w, ln_b, w, bias[, cos, sin]): layernorm over x's last axis, then
+    matmul_epilogue of the result (a build extension, `fuse_layernorm`)."""
+    x, g, b = inputs[:3]
+    _norm_infer((x, g, b), attrs)
+    return _matmul_epilogue_infer((x,) + tuple(inputs[3:]), attrs)
+
+
 def _cast_infer(inputs, attrs):
     dtype = attrs["dtype"]
     if dtype not in DTYPES:
@@ -175,5 +183,6 @@ for _kind, _fn in (
     ("rope_2d", _rope_infer),
     ("attention", _attention_infer),
     ("rope_2d_qk", _rope_qk_infer),
+    ("layernorm_matmul_epilogue", _ln_matmul_infer),
 ):
     register(OpDef(kind=_kind, infer=_fn))

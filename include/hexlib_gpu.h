@@ -249,6 +249,15 @@ void attention_qk_v_fp16(const hexlib_hf *qk, const hexlib_hf *qkv, hexlib_hf *o
  * (KIND 23): the output of matmul_epilogue_f16wt_rope_fp16. */
 void attention_qkv_fp16(const hexlib_hf *qkv, hexlib_hf *out, int rows, int H, int D, int batch,
                         float scale);
+/* layernorm_fp16 over the K features of each row of x [M, K] (fp32 ln_w,
+ * ln_b, eps), rounded to fp16, then matmul_epilogue_f16wt_fp16 on the result
+ * (KIND 24) -- one launch, bit-identical to the two calls. No reference
+ * counterpart: the fusion of kernels/layernorm_fp16/kernel_api.h:38-39 into
+ * the linear that consumes it. Requires 512 <= K <= 768, K % 64 == 0,
+ * 16-byte aligned x and wt; else a no-op. */
+void layernorm_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const float *ln_w, const float *ln_b,
+                                          const hexlib_hf *wt, const float *bias, hexlib_hf *out,
+                                          int M, int K, int N, int act, float eps);
 
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
@@ -273,6 +282,7 @@ int attention_qkv_fp16_entry(const hexlib_args *a);
 int attention_fp16_entry(const hexlib_args *a);
 int attention_qk_v_fp16_entry(const hexlib_args *a);
 int rope_2d_qk_fp16_entry(const hexlib_args *a);
+int layernorm_matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

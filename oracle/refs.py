@@ -170,10 +170,22 @@ def rope_2d_qk(arrays, attrs):
     return (np.stack([q, k], axis=1),)
 
 
+def layernorm_matmul_epilogue(arrays, attrs):
+    """layernorm (elementwise.py:82-95) over x's rows, stored at `ln_round`,
+    then matmul_epilogue (fused.py:44-53, with this build's rope form) of the
+    stored result -- the two ops `fuse_layernorm` replaces."""
+    x, g, b = arrays[:3]
+    (y,) = layernorm((x, g, b), {"eps": attrs["eps"]})
+    if attrs.get("ln_round") == "fp16":
+        y = y.astype(np.float16).astype(y.dtype)
+    return matmul_epilogue((y,) + tuple(arrays[3:]), attrs)
+
+
 REFERENCES = {
     "add": add, "scale": scale, "layernorm": layernorm, "rmsnorm": rmsnorm,
     "gelu_tanh": gelu_tanh, "gelu_erf": gelu_erf, "softmax": softmax,
     "matmul": matmul, "matmul_epilogue": matmul_epilogue, "cast": cast,
     "transpose": transpose, "reshape": reshape, "patchify": patchify,
     "rope_2d": rope_2d, "attention": attention, "rope_2d_qk": rope_2d_qk,
+    "layernorm_matmul_epilogue": layernorm_matmul_epilogue,
 }

@@ -369,3 +369,55 @@ def test_matmul_epilogue_f16wt_rope_invalid_is_a_silent_no_op(dev):
                                                 dev.ptr(out), M, kk, N, 0, hh, dd)
     dev.check()
     assert (dev.down(out) == 7).all()
+
+
+def _ln_inputs(r, M, Kd):
+    x = h16(r.standard_normal((M, Kd)) * 2.0 + 0.5)
+    g = (1.0 + 0.1 * r.standard_normal(Kd)).astype(np.float32)
+    b = (0.1 * r.standard_normal(Kd)).astype(np.float32)
+    return x, g, b
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 3072, 1), (256, 768, 2304, 0), (65, 512, 200, 2),
+                                        (784, 768, 3072, 1), (130, 640, 96, 0), (1, 768, 64, 1)])
+def test_layernorm_matmul_epilogue(dev, M, Kd, N, act):
+    """KIND 24: layernorm_fp16 over K, then the W^T linear, in one launch with
+    the normalised row block resident in LDS. Bit-identical to layernorm_fp16
+    followed by matmul_epilogue_f16wt_fp16 on the same (64x64, one split)
+    tile; the LayerNorm within its harness tolerance of the oracle."""
+    r = rng(31)
+    x, g, b = _ln_inputs(r, M, Kd)
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    dx, dg, db_, dw, dbias = dev.up(x), dev.up(g), dev.up(b), dev.up(np.ascontiguousarray(w.T)), dev.up(bias)
+    dy = dev.empty((M, Kd), np.float16)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(64, 64, 1, 2) == 1
+    try:
+        dev.lib.layernorm_fp16(dev.ptr(dx), dev.ptr(dg), dev.ptr(db_), dev.ptr(dy), M, Kd, 1e-6)
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(dy), dev.ptr(dw), dev.ptr(dbias), dev.ptr(d1), M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    dev.lib.layernorm_matmul_epilogue_f16wt_fp16(dev.ptr(dx), dev.ptr(dg), dev.ptr(db_), dev.ptr(dw), dev.ptr(dbias),
+                                                 dev.ptr(d2), M, Kd, N, act, 1e-6)
+    dev.check()
+    np.testing.assert_array_equal(dev.down(d2).view(np.uint16), dev.down(d1).view(np.uint16))
+    y = dev.down(dy)
+    assert K.close_f16(y, K.layernorm_fp16(x, g, b, 1e-6), 0.02, 1e-3).all()
+    assert K.close_f16(dev.down(d1), K.matmul_epilogue_f16w(y, w, bias, act), 1e-2, 1e-3).all()
+
+
+def test_layernorm_matmul_epilogue_invalid_is_a_silent_no_op(dev):
+    """Feature counts the resident row block does not hold leave the output
+    untouched."""
+    M, N = 64, 64
+    out = dev.up(np.full((M, N), 7, np.float16))
+    for Kd in (448, 832, 600):
+        x = dev.up(np.zeros((M, Kd), np.float16))
+        g, b = dev.up(np.ones(Kd, np.float32)), dev.up(np.zeros(Kd, np.float32))
+        w, bias = dev.up(np.zeros((N, Kd), np.float16)), dev.up(np.zeros(N, np.float32))
+        dev.lib.layernorm_matmul_epilogue_f16wt_fp16(dev.ptr(x), dev.ptr(g), dev.ptr(b), dev.ptr(w), dev.ptr(bias),
+                                                     dev.ptr(out), M, Kd, N, 0, 1e-6)
+    dev.check()
+    assert (dev.down(out) == 7).all()

@@ -29,9 +29,11 @@ def session(torch_gpu):
     s.close()
 
 
-def _run_plan(session, cfg, feeds, graph_mode, weight_layout=None, repeats=1, residual=False, rope=False):
+def _run_plan(session, cfg, feeds, graph_mode, weight_layout=None, repeats=1, residual=False, rope=False,
+              layernorm=False):
     g = E.build_vision_encoder(cfg)
-    wb = build_whole_plan_batch(g, feeds, weight_layout=weight_layout, residual=residual, rope=rope)
+    wb = build_whole_plan_batch(g, feeds, weight_layout=weight_layout, residual=residual, rope=rope,
+                                layernorm=layernorm)
     plan = GpuPlan(wb, session)
     try:
         outs = []
@@ -215,18 +217,21 @@ def test_interpreter_backends_every_kind(session):
     assert K.close_f16(got, want, 0.01, 3e-4).all()
 
 
-@pytest.mark.parametrize("image,batch,mode,residual,rope", [
-    (256, 1, "fused", False, False), (448, 1, "fused", False, False), (256, 4, "fused", False, False),
-    (256, 1, "fused_qkv_rope", False, False), (448, 1, "fused_qkv_rope", False, False),
-    (256, 4, "fused_qkv_rope", False, False),
-    (256, 1, "fused_qkv_rope", True, False), (448, 1, "fused_qkv_rope", True, False),
-    (256, 4, "fused_qkv_rope", True, False),
-    (256, 1, "fused_qkv_rope", True, True), (448, 1, "fused_qkv_rope", True, True),
-    (256, 4, "fused_qkv_rope", True, True), (256, 1, "fused_qkv_rope", False, True)])
-def test_fused_attention_encoder_matches_the_reference_graph(session, image, batch, mode, residual, rope):
+@pytest.mark.parametrize("image,batch,mode,residual,rope,ln", [
+    (256, 1, "fused", False, False, False), (448, 1, "fused", False, False, False),
+    (256, 4, "fused", False, False, False),
+    (256, 1, "fused_qkv_rope", False, False, False), (448, 1, "fused_qkv_rope", False, False, False),
+    (256, 4, "fused_qkv_rope", False, False, False),
+    (256, 1, "fused_qkv_rope", True, False, False), (448, 1, "fused_qkv_rope", True, False, False),
+    (256, 4, "fused_qkv_rope", True, False, False),
+    (256, 1, "fused_qkv_rope", True, True, False), (448, 1, "fused_qkv_rope", True, True, False),
+    (256, 4, "fused_qkv_rope", True, True, False), (256, 1, "fused_qkv_rope", False, True, False),
+    (256, 1, "fused_qkv_rope", True, True, True), (448, 1, "fused_qkv_rope", True, True, True),
+    (256, 4, "fused_qkv_rope", True, True, True), (256, 1, "fused", False, False, True)])
+def test_fused_attention_encoder_matches_the_reference_graph(session, image, batch, mode, residual, rope, ln):
     """The plan with one fused attention op per block (and, with `residual`
-    / `rope`, those folded into the linears) against the storage-rounding
-    oracle of the REFERENCE graph (unfused attention chain): the
+    / `rope` / `ln`, those folded into the linears) against the storage-
+    rounding oracle of the REFERENCE graph (unfused attention chain): the
     whole-encoder bar, <= 2e-2 max abs."""
     base = E.QWEN35_VISION_FP16 if image == 256 else E.encoder_at(image)
     cfg_ref = replace(base, batch=batch)
@@ -235,11 +240,11 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     cfg = replace(cfg_ref, attention=mode)
     fused_feeds = E.fuse_qkv_feeds(feeds, cfg) if mode == "fused_qkv_rope" else feeds
     (out,), wb = _run_plan(session, cfg, fused_feeds, graph_mode=True, residual=residual, rope=rope,
-                           weight_layout="auto" if residual or rope else None)
+                           layernorm=ln, weight_layout="auto" if residual or rope or ln else None)
     assert wb.n_ops == (259 - 12 * (8 if mode == "fused" else 11) - (24 if residual else 0)
-                        - (12 if rope else 0))
+                        - (12 if rope else 0) - (12 if ln else 0))
     want = _oracle(cfg_ref, feeds)
     err = np.abs(out - want).max()
-    print(f"[{mode} residual={residual} rope={rope} {image} b{batch}] max abs vs reference graph {err:.3e}",
-          flush=True)
+    print(f"[{mode} residual={residual} rope={rope} ln={ln} {image} b{batch}] max abs vs reference graph "
+          f"{err:.3e}", flush=True)
     assert err <= 2e-2

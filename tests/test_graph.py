@@ -272,3 +272,34 @@ def test_fuse_rope():
 def KIND_ID_OF(name):
     from hexlib_amd.exec.runner import KIND_ID
     return KIND_ID[name]
+
+
+def test_fuse_layernorm():
+    """Each block's LN2 folds into fc1, the linear it feeds. LN1 feeds the
+    q/k/v linear whose rope tables would give the fused op seven sources, one
+    more than a wire op carries, so it stays; so does the final LayerNorm,
+    which feeds the merger's reshape. On the storage-rounding oracle the output
+    is unchanged bit for bit. Feature counts outside 512..768, more rows than
+    the limit, and q4_0 weights do not fold."""
+    from dataclasses import replace as _replace
+    from hexlib_amd.graph.fuse import fuse_layernorm, fuse_residual, fuse_rope
+    from oracle import eager
+    cfg = _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
+    g = E.build_vision_encoder(cfg)
+    f = fuse_residual(fuse_rope(fuse(g)))
+    r = fuse_layernorm(f)
+    assert len(f.ops) - len(r.ops) == cfg.depth
+    assert sum(1 for o in r.ops if o.kind == "layernorm") == cfg.depth + 1
+    assert sum(1 for o in r.ops if o.kind == "layernorm_matmul_epilogue") == cfg.depth
+    feeds = E.synthetic_feeds(g, cfg, seed=8)
+    np.testing.assert_array_equal(eager.run_stored(f, feeds)[g.outputs[0]],
+                                  eager.run_stored(r, feeds)[g.outputs[0]])
+    assert fuse_layernorm(f, max_rows=255) is f
+    tiny = fuse(E.build_vision_encoder(E.TINY_ENCODER))
+    assert fuse_layernorm(tiny) is tiny                     # hidden size below 512
+    q4 = fuse(E.build_vision_encoder(_replace(E.QWEN35_VISION_FP16, weight_dtype="q4_0")))
+    assert fuse_layernorm(q4) is q4
+    wb = WP.build_whole_plan_batch(g, E.synthetic_feeds(g, cfg), residual=True, rope=True, layernorm=True)
+    assert wb.n_ops == 259 - 12 * 11 - 24 - 12 - 12
+    assert sum(1 for s in wb.op_specs if s == "layernorm_matmul_epilogue_f16wt") == 12
+    assert KIND_ID_OF("layernorm_matmul_epilogue_f16wt") == 24

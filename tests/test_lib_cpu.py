@@ -336,3 +336,16 @@ def test_col_major_rope_staging_matches_the_oracle_permutation():
             blk = got[h * d:(h + 1) * d]
             np.testing.assert_array_equal(blk[0::2], w.T[h * d:h * d + d // 2])
             np.testing.assert_array_equal(blk[1::2], w.T[h * d + d // 2:(h + 1) * d])
+
+
+@pytest.mark.parametrize("M,K,N,want", [(256, 768, 3072, "OK"), (65, 512, 200, "OK"), (64, 640, 64, "OK"),
+                                        (64, 448, 64, "ERR_INVAL_PARAMS"),     # row block below 512
+                                        (64, 832, 64, "ERR_INVAL_PARAMS"),     # row block past 768
+                                        (64, 600, 64, "ERR_INVAL_PARAMS")])    # K not a multiple of 64
+def test_layernorm_matmul_entry_checks(sess, M, K, N, want):
+    blob, size = _blob("layernorm_matmul_epilogue_f16wt",
+                       [((M, K), "fp16", "row_major"), ((K,), "fp32", "row_major"), ((K,), "fp32", "row_major"),
+                        ((K, N), "fp16", "col_major"), ((N,), "fp32", "row_major"), ((M, N), "fp16", "row_major")],
+                       (1, wire.float_param(1e-6)), 5)
+    assert sess.mmap(3, size) == OK
+    assert sess.invoke(blob)[0] == wire.STATUS[want]
