@@ -15,7 +15,8 @@
 // probabilities are rounded to fp16 for the P.V product, accumulated in fp32;
 // the output is divided by the fp32 sum and rounded to fp16 once.
 //
-// Structure: a workgroup of WAVES waves owns 32 queries of one (image, head);
+// Structure: a workgroup of WAVES (4, or 8 when the grid would leave CUs idle)
+// waves owns 32 queries of one (image, head);
 // wave w takes key tiles w, w + WAVES, ... (32 keys each), with the next
 // tile's K and V loads issued before the current tile is computed, and keeps
 // its own running max, sum and output. The waves' partial results are merged
@@ -46,7 +47,7 @@ namespace {
 constexpr int QT = 32;          // queries per wave
 constexpr int KT = 32;          // keys per tile
 constexpr int VT_STRIDE = 40;   // halves per LDS row of V^T
-constexpr int WAVES = 4;        // waves sharing one query tile, splitting its keys
+constexpr int CUS = 256;        // MI355X compute units
 
 __device__ __forceinline__ int kperm(int r) {
     return 16 * (r >> 4) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
@@ -218,8 +219,14 @@ void launch(const hexlib_hf *q, const hexlib_hf *k, long long ldqk, const hexlib
     const auto *K = reinterpret_cast<const f16 *>(k);
     const auto *V = reinterpret_cast<const f16 *>(v);
     auto *O = reinterpret_cast<f16 *>(out);
-    if (D == 64) HX_LAUNCH((attn_fwd<64, WAVES>), grid, dim3(64 * WAVES), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
-    else HX_LAUNCH((attn_fwd<32, WAVES>), grid, dim3(64 * WAVES), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
+    // Fewer workgroups than CUs (one 256-token image): 8 waves split each
+    // query tile's keys, halving every wave's serial chain; otherwise 4, which
+    // keeps two workgroups per CU.
+    const bool wide = (long long) grid.x * grid.y < CUS;
+    if (D == 64 && wide) HX_LAUNCH((attn_fwd<64, 8>), grid, dim3(64 * 8), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
+    else if (D == 64) HX_LAUNCH((attn_fwd<64, 4>), grid, dim3(64 * 4), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
+    else if (wide) HX_LAUNCH((attn_fwd<32, 8>), grid, dim3(64 * 8), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
+    else HX_LAUNCH((attn_fwd<32, 4>), grid, dim3(64 * 4), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e);
 }
 
 bool dims_ok(int rows, int H, int D, int batch) {

@@ -575,6 +575,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
 
+    // The plain epilogue's bias, loaded before the K loop so its latency is
+    // hidden (one column block per wave only: more would cost occupancy).
+    constexpr bool BIAS_EARLY = TN == 1 && !ROPE;
+    float bearly[BIAS_EARLY ? 4 : 1][4];
+    if constexpr (BIAS_EARLY) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int n = n0 + wn + g * 8 + (lane >> 5) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bearly[g][e] = (p.bias && p.splits == 1 && n + e < p.N) ? p.bias[n + e] : 0.0f;
+        }
+    }
+
     auto issue = [&](int kt, int st) {
         if constexpr (!LN) lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kbeg + kt * BK, sA[st]);
         lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kbeg + kt * BK, sB[st]);
@@ -617,25 +630,36 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
             if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (st + STAGES - 1) % STAGES);
             const f16 *as = LN ? sA[kt] : sA[st];
             const f16 *bs = sB[st];
+            // QB k-steps of 16 at a time: all their LDS reads are issued before
+            // the first of their MFMAs (the scheduling barrier keeps them there),
+            // so one LDS latency covers QB steps instead of each step waiting on
+            // its own reads. The MFMA order is the plain k, j, i order.
+            constexpr int QB = TM + TN <= 2 ? 4 : 2;
 #pragma unroll
-            for (int ks = 0; ks < BK; ks += 16) {
-                const int c = (ks >> 3) + (lane >> 5);   // 16-byte chunk of this lane's 8 k
-                f16x8 wf[TN], xf[TM];
+            for (int q0 = 0; q0 < BK / 16; q0 += QB) {
+                f16x8 wf[QB][TN], xf[QB][TM];
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int r = wn + j * 32 + (lane & 31);
-                    wf[j] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
+                for (int q = 0; q < QB; ++q) {
+                    const int c = 2 * (q0 + q) + (lane >> 5);   // 16-byte chunk of this lane's 8 k
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const int r = wn + j * 32 + (lane & 31);
+                        wf[q][j] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const int r = wm + i * 32 + (lane & 31);
+                        xf[q][i] = *reinterpret_cast<const f16x8 *>(as + r * DS_ROW + ((c ^ swz(r)) << 3));
+                    }
                 }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const int r = wm + i * 32 + (lane & 31);
-                    xf[i] = *reinterpret_cast<const f16x8 *>(as + r * DS_ROW + ((c ^ swz(r)) << 3));
-                }
+                for (int q = 0; q < QB; ++q)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
+                    for (int j = 0; j < TN; ++j)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i)
-                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+                        for (int i = 0; i < TM; ++i)
+                            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[q][j], xf[q][i], acc[j][i], 0, 0, 0);
             }
         }
     }
@@ -741,7 +765,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
             const int n = n0 + wn + j * 32 + g * 8 + (lane >> 5) * 4;
             float bv[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
+            for (int e = 0; e < 4; ++e)
+                bv[e] = BIAS_EARLY ? bearly[BIAS_EARLY ? g : 0][e] : (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int m = m0 + wm + i * 32 + (lane & 31);
