@@ -555,6 +555,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     constexpr int LOADS = (LN ? BN : BM + BN) / (8 * NW);
     static_assert(STAGES >= 2 && LOADS * (STAGES - 2) <= 63, "vmcnt holds at most 63");
     static_assert(!LN || (BM / (8 * NW)) * LN_KT + LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
+    // one 32x32 block per wave: the software-pipelined loop (see below)
+    constexpr bool PIPE = TM == 1 && TN == 1 && !LN;
+    static_assert(!PIPE || LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
     __shared__ __attribute__((aligned(16))) f16 sA[LN ? LN_KT : STAGES][BM * DS_ROW];
     __shared__ __attribute__((aligned(16))) f16 sB[STAGES][BN * DS_ROW];
 
@@ -607,12 +610,60 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
         else ln_rows_in_lds<BM, NW, 1>(sA, p);
         HX_WAIT_LGKM0();
         __builtin_amdgcn_s_barrier();
-    } else {
+    } else if constexpr (!PIPE) {
 #pragma unroll
         for (int s = 0; s < STAGES - 1; ++s)
             if (s < KT) issue(s, s);
     }
 
+    if constexpr (PIPE) {
+        // One 32x32 block per wave: the ring holds one more slice in flight, and
+        // slice kt + 1's fragments are read from LDS while slice kt's MFMAs run
+        // (two register sets). Slot kt % STAGES is refilled with slice
+        // kt + STAGES once every wave has read it (the barrier after its MFMAs
+        // were issued: their operands had arrived). Same MFMA order as below.
+        struct Frags {
+            f16x8 w[BK / 16], x[BK / 16];
+        };
+        const int rb = wn + (lane & 31), ra = wm + (lane & 31);
+        auto read = [&](int kt, Frags &f) {
+            const int slot = kt % STAGES;
+            const f16 *as = sA[slot], *bs = sB[slot];
+#pragma unroll
+            for (int q = 0; q < BK / 16; ++q) {
+                const int c = 2 * q + (lane >> 5);
+                f.w[q] = *reinterpret_cast<const f16x8 *>(bs + rb * DS_ROW + ((c ^ swz(rb)) << 3));
+                f.x[q] = *reinterpret_cast<const f16x8 *>(as + ra * DS_ROW + ((c ^ swz(ra)) << 3));
+            }
+        };
+        auto step = [&](int kt, const Frags &cur, Frags &nxt) {
+#pragma unroll
+            for (int q = 0; q < BK / 16; ++q)
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.w[q], cur.x[q], acc[0][0], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + 1 < KT) {
+                // slice kt + 1 is complete for this wave once at most the slices
+                // issued after it remain outstanding
+                if (kt + STAGES <= KT) HX_WAIT_VMCNT(LOADS * (STAGES - 2));
+                else HX_WAIT_VMCNT(0);
+                __builtin_amdgcn_s_barrier();
+                if (kt + STAGES < KT) issue(kt + STAGES, kt % STAGES);
+                read(kt + 1, nxt);
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < STAGES; ++s)
+            if (s < KT) issue(s, s);
+        if (KT >= STAGES) HX_WAIT_VMCNT(LOADS * (STAGES - 1));
+        else HX_WAIT_VMCNT(0);
+        __builtin_amdgcn_s_barrier();
+        Frags f0, f1;
+        if (KT > 0) read(0, f0);
+        for (int kt = 0; kt < KT; kt += 2) {
+            step(kt, f0, f1);
+            if (kt + 1 < KT) step(kt + 1, f1, f0);
+        }
+    } else
     for (int kt0 = 0; kt0 < KT; kt0 += STAGES) {
 #pragma unroll
         for (int st = 0; st < STAGES; ++st) {
