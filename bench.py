@@ -509,7 +509,9 @@ def main() -> int:
         for label, vcfg, steps in (("256_b32", replace(cfg, batch=32), max(5, args.steps // 10)),
                                    ("448_b1", replace(E.encoder_at(448), attention="fused_qkv_rope"),
                                     max(10, args.steps // 2)),
-                                   ("256_b1_reference_graph", E.QWEN35_VISION_FP16, max(10, args.steps // 2))):
+                                   ("256_b1_reference_graph", E.QWEN35_VISION_FP16, max(10, args.steps // 2)),
+                                   ("256_b1_q8_0", replace(E.QWEN35_VISION_Q8, attention="fused_qkv_rope"),
+                                    max(10, args.steps // 2))):
             log(f"variant {label}")
             try:
                 variants[label] = run_variant(session, vcfg, steps, label)

@@ -18,6 +18,7 @@
 // registers before the current slice's MFMAs and written to the other LDS
 // buffer afterwards: one barrier per slice. B arrives in one of five layouts
 // and is converted to [n][k] on its way into LDS:
+//   B_Q8K q8_0 [N][K/32] 34-B blocks -- dequantize, 16-byte LDS writes
 //   B_KN  fp16 [K, N]                -- 16-byte loads along n, 2-byte LDS scatter
 //   B_NK  fp16 [N, K] (W^T)          -- 16-byte loads and 16-byte LDS writes
 //   B_Q4N q4_0 [K][N/32] 18-B blocks -- dequantize, 2-byte LDS scatter
@@ -49,7 +50,7 @@ constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // halves per LDS row (144 B)
 constexpr int MAX_SPLITS = 16;      // split-K factor limit (splitk_reduce unrolls to it)
 
-enum BMode { B_KN = 0, B_NK = 1, B_Q4N = 2, B_Q4K = 3 };
+enum BMode { B_KN = 0, B_NK = 1, B_Q4N = 2, B_Q4K = 3, B_Q8K = 4 };
 
 struct GemmArgs {
     const f16 *A;
@@ -147,6 +148,19 @@ __device__ __forceinline__ void load_q4_block(const uint8_t *p, float &d, uint32
     for (int i = 0; i < 4; ++i) qs[i] = (uint32_t) h[1 + 2 * i] | ((uint32_t) h[2 + 2 * i] << 16);
 }
 
+// Half a q8_0 block (16 int8 at byte 2 + 16 * half, 2-byte aligned) and its scale.
+__device__ __forceinline__ void load_q8_half(const uint8_t *p, int half, float &d, uint32_t qs[4]) {
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+    d = (float) __builtin_bit_cast(f16, h[0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[i] = (uint32_t) h[1 + 8 * half + 2 * i] | ((uint32_t) h[2 + 8 * half + 2 * i] << 16);
+}
+
+// q * d rounded once to fp16 (the product of an int8 and an fp16 is exact in fp32).
+__device__ __forceinline__ f16 q8_val(float d, const uint32_t qs[4], int j) {
+    return (f16) (d * (float) (int8_t) ((qs[j >> 2] >> ((j & 3) * 8)) & 0xFF));
+}
+
 __device__ __forceinline__ int nib(const uint32_t qs[4], int j, int shift) {
     return (int) ((qs[j >> 2] >> ((j & 3) * 8 + shift)) & 0xF);
 }
@@ -161,8 +175,8 @@ struct Gemm {
     static constexpr int Q4K_ITEMS_ALL = BN * (BK / 32) * 2;   // (n, block, half)
     static constexpr int Q4N_ITEMS = (Q4N_ITEMS_ALL + TPB - 1) / TPB;
     static constexpr int Q4K_ITEMS = (Q4K_ITEMS_ALL + TPB - 1) / TPB;
-    static constexpr int B_ITEMS = MODE == B_Q4N ? Q4N_ITEMS : MODE == B_Q4K ? Q4K_ITEMS : B_VECS;
-    static constexpr bool Q4 = MODE == B_Q4N || MODE == B_Q4K;
+    static constexpr int B_ITEMS = MODE == B_Q4N ? Q4N_ITEMS : (MODE == B_Q4K || MODE == B_Q8K) ? Q4K_ITEMS : B_VECS;
+    static constexpr bool Q4 = MODE == B_Q4N || MODE == B_Q4K || MODE == B_Q8K;   // block-quantized B
 
     struct Regs {
         f16x8 a[A_VECS];
@@ -242,7 +256,7 @@ struct Gemm {
                 if (it < Q4N_ITEMS_ALL && k < kend && n < p.N)
                     load_q4_block(W + (long long) k * p.ldb + (long long) (n / 32) * 18, r.qd[i], r.qs[i]);
             }
-        } else {
+        } else if constexpr (MODE == B_Q4K) {
             const uint8_t *W = reinterpret_cast<const uint8_t *>(Bv);
 #pragma unroll
             for (int i = 0; i < Q4K_ITEMS; ++i) {
@@ -254,6 +268,20 @@ struct Gemm {
                 r.qs[i][0] = r.qs[i][1] = r.qs[i][2] = r.qs[i][3] = 0x88888888u;
                 if (it < Q4K_ITEMS_ALL && n < p.N && k < kend)
                     load_q4_block(W + (long long) n * p.ldb + (long long) (k / 32) * 18, r.qd[i], r.qs[i]);
+            }
+        } else {
+            // q8_0 along K of W^T: item = (n, block, half), 16 int8 each
+            const uint8_t *W = reinterpret_cast<const uint8_t *>(Bv);
+#pragma unroll
+            for (int i = 0; i < Q4K_ITEMS; ++i) {
+                const int it = threadIdx.x + i * TPB;
+                const int blk = it >> 1, half = it & 1;
+                const int nr = blk / (BK / 32), kb = blk % (BK / 32);
+                const int n = n0 + nr, k = k0 + kb * 32;
+                r.qd[i] = 0.0f;
+                r.qs[i][0] = r.qs[i][1] = r.qs[i][2] = r.qs[i][3] = 0u;
+                if (it < Q4K_ITEMS_ALL && n < p.N && k < kend)
+                    load_q8_half(W + (long long) n * p.ldb + (long long) (k / 32) * 34, half, r.qd[i], r.qs[i]);
             }
         }
     }
@@ -302,8 +330,13 @@ struct Gemm {
                 f16x8 lo, hi;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    lo[j] = q4_val(r.qd[i], nib(r.qs[i], j, half * 4));
-                    hi[j] = q4_val(r.qd[i], nib(r.qs[i], j + 8, half * 4));
+                    if constexpr (MODE == B_Q8K) {
+                        lo[j] = q8_val(r.qd[i], r.qs[i], j);
+                        hi[j] = q8_val(r.qd[i], r.qs[i], j + 8);
+                    } else {
+                        lo[j] = q4_val(r.qd[i], nib(r.qs[i], j, half * 4));
+                        hi[j] = q4_val(r.qd[i], nib(r.qs[i], j + 8, half * 4));
+                    }
                 }
                 f16 *dst = Bs + nr * LDS_STRIDE + kb * 32 + half * 16;
                 *reinterpret_cast<f16x8 *>(dst) = lo;
@@ -1347,6 +1380,15 @@ extern "C" void matmul_epilogue_fp16(const hexlib_hf *a, const unsigned char *w,
     if (!a || !w || !out || !dims_ok(M, K, N, 1) || N % 32 || act < 0 || act > 2) return;
     if (!hx::aligned(w, 2)) return;
     launch<B_Q4N>(args(a, K, 0, w, (long long) (N / 32) * 18, 0, bias, out, N, 0, M, N, K, act), 1,
+                  K % 8 == 0 && hx::aligned(a, 16), false);
+}
+
+extern "C" void matmul_epilogue_q8k_fp16(const hexlib_hf *a, const unsigned char *wt,
+                                         const float *bias, hexlib_hf *out, int M, int K, int N,
+                                         int act) {
+    if (!a || !wt || !out || !dims_ok(M, K, N, 1) || K % 32 || act < 0 || act > 2) return;
+    if (!hx::aligned(wt, 2)) return;
+    launch<B_Q8K>(args(a, K, 0, wt, (long long) (K / 32) * 34, 0, bias, out, N, 0, M, N, K, act), 1,
                   K % 8 == 0 && hx::aligned(a, 16), false);
 }
 

@@ -94,6 +94,10 @@ QWEN35_VISION_FP16 = VitConfig(
 # q4_0 weights.
 QWEN35_VISION_Q4 = replace(QWEN35_VISION_FP16, temporal_patch_size=2, weight_dtype="q4_0")
 
+# q8_0 weights (the reference's README measures q8_0 at cosine 0.999 against
+# q4_0's 0.868 on the real model, `README.md:180-191`) on the cfg-4 shape.
+QWEN35_VISION_Q8 = replace(QWEN35_VISION_FP16, weight_dtype="q8_0")
+
 # BASELINE cfg 1: the tiny encoder run through the CPU reference executor.
 TINY_ENCODER = VitConfig(
     depth=2, hidden_size=64, num_heads=2, intermediate_size=256, patch_size=16,

@@ -28,7 +28,7 @@ from hexlib_amd import lib as _lib
 from hexlib_amd.exec import wire
 from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, select
 from hexlib_amd.exec.wholeplan import ALIGN, WholePlanBatch, align_up, decode, stage_col_major_rope
-from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
+from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked, pack_q8_0_kgrouped
 
 
 class GpuError(RuntimeError):
@@ -200,7 +200,8 @@ class GpuBackend:
                 else:
                     arr = np.asarray(a, dtype=np.float32)
                     shape = arr.shape
-                    data = pack_q4_0_kgrouped(arr) if lays[i] == "q4_0_kgroup" else pack_q4_0_nblocked(arr)
+                    data = (pack_q8_0_kgrouped(arr) if lays[i] == "q8_0_kgroup" else
+                            pack_q4_0_kgrouped(arr) if lays[i] == "q4_0_kgroup" else pack_q4_0_nblocked(arr))
             else:
                 arr = np.ascontiguousarray(a, dtype=np.float16 if dt == "fp16" else np.float32)
                 shape = arr.shape

@@ -53,6 +53,7 @@ KIND_ID: dict[str, int] = {
     "matmul_epilogue_f16wt_rope": 22,
     "attention_qkv": 23,
     "layernorm_matmul_epilogue_f16wt": 24,
+    "matmul_epilogue_q8k": 25,
 }
 
 
@@ -236,6 +237,15 @@ SPECS: dict[str, RunnerSpec] = {
         weight=(1, "q4_0"), primary=False,
         notes="q4_0 weight, logical [K, N] on the wire, stored as W^T [N, K] blocked along K",
         rank=2),
+    "matmul_epilogue_q8k": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_q8k_fp16", ("fp16", "q8_0", "fp32"), "fp16",
+        _MM_SCALARS,
+        layouts=("row_major", "q8_0_kgroup", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),
+        checks=("K % 32 == 0", "((uintptr_t)a->buf[1] & 1) == 0"),
+        weight=(1, "q8_0"), primary=False,
+        notes="extension: q8_0 weight, logical [K, N] on the wire, stored as W^T [N, K] blocked along K "
+              "(the reference has the dtype, no kernel)"),
     "matmul_epilogue_f16w": RunnerSpec(
         "matmul_epilogue", "matmul_epilogue_f16w_fp16", ("fp16", "fp16", "fp32"), "fp16",
         _MM_SCALARS, extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),

@@ -35,7 +35,7 @@ from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, RunnerSpec, select
 from hexlib_amd.graph.fuse import fuse, fuse_layernorm, fuse_residual, fuse_rope
 from hexlib_amd.graph.ir import Graph
 from hexlib_amd.graph.ir import nbytes as ir_nbytes
-from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
+from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked, pack_q8_0_kgrouped
 
 ALIGN = 256
 _NP = {"fp32": np.float32, "fp16": np.float16, "int32": np.int32}
@@ -262,6 +262,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                 data = bytes(value)
             elif p.layout == "q4_0_kgroup":
                 data = pack_q4_0_kgrouped(np.asarray(value))
+            elif p.layout == "q8_0_kgroup":
+                data = pack_q8_0_kgrouped(np.asarray(value))
             else:
                 data = pack_q4_0_nblocked(np.asarray(value))
         elif p.layout == "col_major_rope":

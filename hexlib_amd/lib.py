@@ -37,6 +37,7 @@ SIGNATURES = {
     "matmul_epilogue_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_f16w_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_q4k_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
+    "matmul_epilogue_q8k_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_f16wt_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_f16wt_res_fp16": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_f16wt_rope_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),

@@ -76,6 +76,7 @@ enum hexlib_dsp_status {
 #define HEXLIB_LAYOUT_Q4_0_KGROUP   3u
 #define HEXLIB_LAYOUT_COL_MAJOR     4u
 #define HEXLIB_LAYOUT_COL_MAJOR_ROPE 5u
+#define HEXLIB_LAYOUT_Q8_0_KGROUP   6u
 
 /* Dtype ids: hexlib/runtime/wire.py:61. */
 #define HEXLIB_DTYPE_FP32  0u
@@ -223,6 +224,16 @@ void matmul_epilogue_f16wt_res_fp16(const hexlib_hf *a, const hexlib_hf *wt, con
 void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char *wt,
                               const float *bias, hexlib_hf *out,
                               int M, int K, int N, int act);
+/* act(a @ deq(w) + bias), w = q8_0 blocks of 32 along K of W^T [N, K]
+ * (34 bytes: fp16 d, 32 int8; hexlib/exec/quant.py:138-220, llama.cpp
+ * block_q8_0), each dequantized weight q * d rounded to fp16 (KIND 25). No
+ * reference kernel: the reference defines the q8_0 dtype
+ * (hexlib/graph/ir.py:15,37-52) and wire id (hexlib/runtime/wire.py:61) but
+ * multiplies it only on the CPU. Requires K % 32 == 0 and a 2-byte aligned w;
+ * else a no-op. bias may be NULL. */
+void matmul_epilogue_q8k_fp16(const hexlib_hf *a, const unsigned char *wt,
+                              const float *bias, hexlib_hf *out,
+                              int M, int K, int N, int act);
 /* Fused full attention (KIND 18): out = softmax(scale * q k^T) v for each of
  * batch images and H heads; q, k, v, out are [rows = batch * T, H, D] fp16
  * (token-major, the layout rope_2d and the linears produce), D = 32 or 64.
@@ -283,6 +294,7 @@ int attention_fp16_entry(const hexlib_args *a);
 int attention_qk_v_fp16_entry(const hexlib_args *a);
 int rope_2d_qk_fp16_entry(const hexlib_args *a);
 int layernorm_matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_q8k_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

@@ -23,6 +23,7 @@ any summation order the GPU picks.
 | matmul_epilogue_fp16 | kernels/matmul_epilogue_fp16/baseline.c:27-97     | _ref (0.01,3e-4) |
 | matmul_epilogue_f16w | hexlib/graph/opdefs/fused.py:44-53 with fp16 w    | reduces to matmul_epilogue_fp16 on dequantized weights |
 | matmul_q4k           | q4_0 blocks along K of W^T, same numerics as q4_0 | reduces to matmul_epilogue_fp16 via a block transpose |
+| matmul_q8k           | q8_0 blocks along K of W^T, weights rounded to fp16 | dequantize_q8_0 pinned by the scalar ggml transcription |
 | attention_fp16       | hexlib/models/vit.py:185-193 chain, fused         | equals the composition of the registry references; uniform / one-hot closed forms |
 | rope_2d_qk_fp16      | rope_2d_fp16 on the q, k slots of a fused qkv     | rope_2d_fp16 (pinned bit-exact) per slot |
 | attention_qk_v_fp16  | attention_fp16 on strided q, k, v                 | attention_fp16 |
@@ -34,7 +35,7 @@ import math
 
 import numpy as np
 
-from oracle.quant import dequantize_q4_0_fp16
+from oracle.quant import dequantize_q4_0_fp16, dequantize_q8_0_fp16
 
 ACT_NONE, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
 _erf = np.vectorize(math.erf, otypes=[np.float64])
@@ -142,6 +143,12 @@ def matmul_epilogue_fp16(a, w_q4, bias, K, N, act):
 
 def matmul_epilogue_f16w(a, w16, bias, act):
     return gemm_epilogue(a, _f32(w16), bias, act)
+
+
+def matmul_q8k(a, wt_q8, bias, K, N, act):
+    """q8_0 blocks along K of the transposed weight: wt_q8 is [N, K] q8_0;
+    each dequantized weight rounded to fp16."""
+    return gemm_epilogue(a, dequantize_q8_0_fp16(wt_q8, (N, K)).T, bias, act)
 
 
 def matmul_q4k(a, wt_q4, bias, K, N, act):

@@ -96,7 +96,7 @@ def matmul_epilogue(arrays, attrs):  # fused.py:44-53
     return (out,)
 
 
-_NUMPY = {"fp32": np.float32, "fp16": np.float32, "int32": np.int32, "q4_0": np.float32}
+_NUMPY = {"fp32": np.float32, "fp16": np.float32, "int32": np.int32, "q4_0": np.float32, "q8_0": np.float32}
 
 
 def cast(arrays, attrs):  # structural.py:81-82 (fp16 is computed as float32)

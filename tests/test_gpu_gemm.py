@@ -421,3 +421,46 @@ def test_layernorm_matmul_epilogue_invalid_is_a_silent_no_op(dev):
                                                      dev.ptr(out), M, Kd, N, 0, 1e-6)
     dev.check()
     assert (dev.down(out) == 7).all()
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(1, 896, 4864, 0), (16, 896, 4864, 0), (256, 896, 4864, 0),
+                                        (256, 4864, 896, 0), (256, 2048, 2048, 0), (256, 768, 3072, 1),
+                                        (70, 96, 40, 2), (300, 768, 2304, 0)])
+def test_matmul_q8k(dev, M, Kd, N, act):
+    """KIND 25: q8_0 blocks along K of W^T -- random int8 codes (including
+    -128) and fp16 scales U(0.005, 0.02) as in cfg 5's q4_0 recipe -- against
+    the oracle's dequantize-to-fp16 product, harness tolerance (0.01, 3e-4)."""
+    r = rng(9)
+    n_blocks = N * Kd // 32
+    blocks = np.empty((n_blocks, 34), np.uint8)
+    blocks[:, :2] = r.uniform(0.005, 0.02, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = r.integers(0, 256, (n_blocks, 32), dtype=np.uint8)
+    wq = blocks.tobytes()
+    a = h16(r.standard_normal((M, Kd)))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dw, db, do = dev.up(a), dev.up(blocks), dev.up(bias), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_q8k_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+    dev.check()
+    got, want = dev.down(do), K.matmul_q8k(a, wq, bias, Kd, N, act)
+    report(f"q8k {M}x{Kd}x{N}", got, want)
+    assert K.close_f16(got, want, 0.01, 3e-4).all()
+
+
+def test_q8k_is_the_f16_gemm_on_its_dequantized_weight(dev):
+    """A q8_0 weight with d = 1 in every block and integer codes dequantizes
+    to those integers exactly; with activations on a quarter grid every
+    partial sum is exact in fp32, so the kernel's output is the exact product
+    rounded once to fp16."""
+    from hexlib_amd.quant import quantize_q8_0
+    r = rng(10)
+    M, Kd, N = 64, 256, 96
+    w = r.integers(-127, 128, (Kd, N)).astype(np.float32)
+    w[::32, :] = 127.0                               # amax 127 in every block along K -> d = 1
+    wq = quantize_q8_0(np.ascontiguousarray(w.T))
+    a = h16(r.integers(-2, 3, (M, Kd)).astype(np.float32) / 4)
+    bias = np.zeros(N, np.float32)
+    da, dw, db, do = dev.up(a), dev.up(np.frombuffer(wq, np.uint8)), dev.up(bias), dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_q8k_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, 0)
+    dev.check()
+    exact = (a.astype(np.float64) @ w.astype(np.float64)).astype(np.float16)
+    np.testing.assert_array_equal(dev.down(do), exact)

@@ -121,6 +121,32 @@ def test_qwen_encoder_reference_q4_config(session, layout):
     assert err <= 2e-2
 
 
+def test_qwen_encoder_q8_0(session):
+    """cfg 4 with q8_0 weights (KIND 25 for every linear). The oracle gets the
+    dequantized, fp16-rounded weights the kernel multiplies with; the output
+    also stays close to the fp16-weight encoder's (cosine > 0.999)."""
+    from hexlib_amd.quant import pack_q8_0_kgrouped
+    from oracle.quant import dequantize_q8_0_fp16
+    cfg = replace(E.QWEN35_VISION_Q8, depth=4)
+    g = E.build_vision_encoder(cfg)
+    feeds = E.synthetic_feeds(g, cfg, seed=1)
+    dense = {}
+    for t in g.tensors.values():
+        if t.dtype == "q8_0":
+            w = feeds[t.name]
+            dense[t.name] = np.ascontiguousarray(dequantize_q8_0_fp16(pack_q8_0_kgrouped(w), w.shape[::-1]).T)
+    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True)
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_q8k") == 6 * cfg.depth + 3
+    want = _oracle(cfg, feeds, dense)
+    err = np.abs(out - want).max()
+    cfg16 = replace(cfg, weight_dtype="fp16")
+    (ref16,), _ = _run_plan(session, cfg16, feeds, graph_mode=True)
+    cos = float(np.dot(out.ravel(), ref16.ravel()) / (np.linalg.norm(out) * np.linalg.norm(ref16)))
+    print(f"[qwen q8_0] max abs vs oracle {err:.3e}; cosine vs fp16 weights {cos:.6f}", flush=True)
+    assert err <= 2e-2
+    assert cos > 0.999
+
+
 def test_batched_encoder_matches_per_image(session):
     cfg1 = E.TINY_ENCODER
     cfgb = replace(cfg1, batch=3)

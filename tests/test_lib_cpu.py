@@ -349,3 +349,14 @@ def test_layernorm_matmul_entry_checks(sess, M, K, N, want):
                        (1, wire.float_param(1e-6)), 5)
     assert sess.mmap(3, size) == OK
     assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+@pytest.mark.parametrize("K,layout,want", [(768, "q8_0_kgroup", "OK"), (96, "q8_0_kgroup", "OK"),
+                                           (768, "q4_0_kgroup", "ERR_REQUIRES")])
+def test_matmul_q8k_entry_checks(sess, K, layout, want):
+    M, N = 16, 64
+    blob, size = _blob("matmul_epilogue_q8k",
+                       [((M, K), "fp16", "row_major"), ((K, N), "q8_0", layout),
+                        ((N,), "fp32", "row_major"), ((M, N), "fp16", "row_major")], (0,), 3)
+    assert sess.mmap(3, size) == OK
+    assert sess.invoke(blob)[0] == wire.STATUS[want]
