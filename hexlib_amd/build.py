@@ -65,9 +65,27 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise BuildError(f"link failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_replay()
     if verbose:
-        print(f"built {LIB_PATH} from {len(objs)} sources")
+        print(f"built {LIB_PATH} from {len(objs)} sources, and {REPLAY_PATH}")
     return LIB_PATH
+
+
+REPLAY_SRC = os.path.join(PKG, "replay", "hxplan_replay.c")
+REPLAY_PATH = os.path.join(PKG, "hxplan_replay")
+
+
+def build_replay() -> str:
+    """The plan-file replay program: plain C against the library (host code
+    only, gcc), found beside it at run time through its rpath."""
+    tmp = REPLAY_PATH + ".tmp"
+    cmd = ["gcc", "-O2", "-std=c11", "-Wall", f"-I{INCLUDE}", REPLAY_SRC, "-o", tmp,
+           f"-L{PKG}", "-lhexlib_gpu", "-Wl,-rpath,$ORIGIN"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise BuildError(f"replay build failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, REPLAY_PATH)
+    return REPLAY_PATH
 
 
 if __name__ == "__main__":

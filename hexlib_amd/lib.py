@@ -63,7 +63,27 @@ SIGNATURES = {
                                ctypes.POINTER(_U32), ctypes.POINTER(_U64)]),
     "hexlib_gpu_invoke": (_I, [_P, ctypes.c_char_p, _U32, _P, _U32, ctypes.POINTER(_U32), _U32]),
     "hexlib_gpu_session_stream": (_P, [_P]),
+    "hexlib_gpu_plan_inspect": (_I, [ctypes.c_char_p, _P]),
+    "hexlib_gpu_plan_load": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "hexlib_gpu_plan_info_of": (_I, [_P, _P]),
+    "hexlib_gpu_plan_io": (_I, [_P, _U32, _P]),
+    "hexlib_gpu_plan_write": (_I, [_P, _U32, _P, _U64]),
+    "hexlib_gpu_plan_read": (_I, [_P, _U32, _P, _U64]),
+    "hexlib_gpu_plan_run": (_I, [_P, _U32, _P, _U32, ctypes.POINTER(_U32)]),
+    "hexlib_gpu_plan_free": (_I, [_P]),
 }
+
+
+class PlanInfo(ctypes.Structure):
+    """hexlib_plan_info (include/hexlib_gpu.h)."""
+    _fields_ = [("version", _U32), ("fd", _U32), ("n_io", _U32), ("n_ops", _U32),
+                ("arena_bytes", _U64), ("const_bytes", _U64), ("blob_bytes", _U64), ("data_bytes", _U64)]
+
+
+class PlanIO(ctypes.Structure):
+    """hexlib_plan_io (include/hexlib_gpu.h)."""
+    _fields_ = [("name", ctypes.c_char * 48), ("role", _U32), ("dtype", _U32), ("offset", _U64),
+                ("nbytes", _U64), ("ne", _U32 * 4), ("data_offset", _U64)]
 
 INVOKE_DRYRUN = 0x1
 INVOKE_TIMED = 0x2

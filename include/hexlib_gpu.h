@@ -345,6 +345,43 @@ int hexlib_gpu_invoke(hexlib_gpu_ctx *ctx, const uint8_t *batch, uint32_t len,
 /* The session's stream (a hipStream_t). */
 void *hexlib_gpu_session_stream(hexlib_gpu_ctx *ctx);
 
+/* ---- 4. whole-plan files ------------------------------------------------
+ * The whole-plan batch (hexlib/exec/wholeplan.py:92-357: arena layout, const
+ * image and wire blob) as an on-disk artefact, replayed through
+ * hexlib_gpu_invoke with no Python on the host. No reference counterpart: the
+ * reference builds the batch in Python for every run
+ * (hexlib/tests/test_wholeplan.py:181-183). hexlib_amd/exec/planfile.py
+ * writes the files; the format is described in hexlib_amd/csrc/planfile.cpp. */
+typedef struct hexlib_plan_info {
+    uint32_t version, fd, n_io, n_ops;
+    uint64_t arena_bytes, const_bytes, blob_bytes, data_bytes;
+} hexlib_plan_info;
+typedef struct hexlib_plan_io {
+    char name[48];           /* the graph tensor's name, NUL-terminated */
+    uint32_t role;           /* 0 = graph input, 1 = graph output */
+    uint32_t dtype;          /* wire dtype id (HEXLIB_DTYPE_*) */
+    uint64_t offset, nbytes; /* its bytes in the arena */
+    uint32_t ne[4];
+    uint64_t data_offset;    /* a stored sample input value, or UINT64_MAX */
+} hexlib_plan_io;
+typedef struct hexlib_gpu_plan hexlib_gpu_plan;
+/* Parses and validates a plan file and dry-runs its blob against a mapping
+ * of the arena (no HIP call): a status, and the sizes and op count. */
+int hexlib_gpu_plan_inspect(const char *path, hexlib_plan_info *info);
+/* On a started session: allocates the arena on the session's device, stages
+ * the const image and the stored sample inputs, and maps the arena under the
+ * blob's fd. The plan owns the arena until hexlib_gpu_plan_free. */
+int hexlib_gpu_plan_load(hexlib_gpu_ctx *ctx, const char *path, hexlib_gpu_plan **out);
+int hexlib_gpu_plan_info_of(const hexlib_gpu_plan *plan, hexlib_plan_info *info);
+int hexlib_gpu_plan_io(const hexlib_gpu_plan *plan, uint32_t i, hexlib_plan_io *io);
+/* Host bytes into input i / out of tensor i; nbytes must equal its size. */
+int hexlib_gpu_plan_write(hexlib_gpu_plan *plan, uint32_t i, const void *host, uint64_t nbytes);
+int hexlib_gpu_plan_read(const hexlib_gpu_plan *plan, uint32_t i, void *host, uint64_t nbytes);
+/* hexlib_gpu_invoke of the plan's blob (same flags, same response). */
+int hexlib_gpu_plan_run(hexlib_gpu_plan *plan, uint32_t flags, uint8_t *rsp, uint32_t rsp_cap,
+                        uint32_t *rsp_len);
+int hexlib_gpu_plan_free(hexlib_gpu_plan *plan);
+
 #ifdef __cplusplus
 }
 #endif
