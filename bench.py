@@ -477,6 +477,9 @@ def main() -> int:
         session.close()
         print(json.dumps({"roofline": roof}))
         return 0
+    # first, as in --roofline-only, so the committed rocprof trace of that mode
+    # describes the same measurement
+    roof = roofline(plan, g)
     sec = time_replays(plan, args.steps, args.warmup)
     ms = sec / args.steps * 1e3
     ips = args.steps * cfg.batch / sec
@@ -495,7 +498,6 @@ def main() -> int:
     except Exception as e:  # noqa: BLE001
         log(f"timed graph replay failed: {e}")
 
-    roof = roofline(plan, g)
     share = roof["launches_per_image"] * roof["avg_launch_ns"] / sum(r["count"] * r["avg_ns"] for r in per_op)
     roof["share_of_plan"] = round(share, 3)
     top = per_op[0]
