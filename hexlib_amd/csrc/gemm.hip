@@ -872,6 +872,109 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     }
 }
 
+// ---- W^T small-M, long-K path: 32x32 tiles, K split across the waves -----------
+//
+// For few rows and a long K (fc2 at batch 1: 256x3072x768) the 64x64 tiles
+// need split-K and a second, reducing launch to fill the chip. Here a
+// 256-thread workgroup owns a 32x32 output tile (192 workgroups for fc2) and
+// walks K in KW_BK = 256-deep stages, each copied HBM->LDS by
+// global_load_lds as four 64-wide sub-slices of A and B rows (the swizzled
+// [row][64] layout of gemm_nk_lds), into a ring of KW_STAGES. Wave w multiplies
+// sub-slice w of every stage into its own 32x32 accumulator, so every LDS
+// fragment is read once per workgroup. The four partial tiles are summed
+// through LDS in wave order 0..3 (fixed, so results are identical run to run)
+// and wave 0 applies the epilogue: bias, activation, one rounding, the
+// optional residual. Requires K % KW_BK == 0 and 16-byte aligned rows.
+constexpr int KW_BK = 256;
+constexpr int KW_STAGES = 3;
+
+__global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
+    constexpr int LOADS = 8;   // wave-instructions per stage: 4 sub-slices x (A + B)
+    static_assert(LOADS * (KW_STAGES - 1) <= 63, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(16))) f16 sA[KW_STAGES][4][32 * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 sB[KW_STAGES][4][32 * DS_ROW];
+    const f16 *A = p.A;
+    const f16 *B = reinterpret_cast<const f16 *>(p.B);
+    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int KT = p.K / KW_BK;
+
+    auto issue = [&](int kt, int st) {
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+            lds_copy_slice<32, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
+            lds_copy_slice<32, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
+        }
+    };
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KW_STAGES - 1; ++s)
+        if (s < KT) issue(s, s);
+    const int r = lane & 31;
+    for (int kt = 0; kt < KT; ++kt) {
+        const int st = kt % KW_STAGES;
+        // stage kt's copies are done (this wave) once at most the later ones remain
+        if (kt + KW_STAGES - 1 <= KT) HX_WAIT_VMCNT(LOADS * (KW_STAGES - 2));
+        else HX_WAIT_VMCNT(0);
+        __builtin_amdgcn_s_barrier();   // and every wave's; stage kt - 1's reads are done
+        if (kt + KW_STAGES - 1 < KT) issue(kt + KW_STAGES - 1, (kt + KW_STAGES - 1) % KW_STAGES);
+        const f16 *as = sA[st][wave], *bs = sB[st][wave];
+        f16x8 wf[BK / 16], xf[BK / 16];
+#pragma unroll
+        for (int q = 0; q < BK / 16; ++q) {
+            const int c = 2 * q + (lane >> 5);
+            wf[q] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
+            xf[q] = *reinterpret_cast<const f16x8 *>(as + r * DS_ROW + ((c ^ swz(r)) << 3));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < BK / 16; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[q], xf[q], acc, 0, 0, 0);
+    }
+    // combine the waves' partial tiles: [wave][e/4][lane][4] floats over stage 0 of sA
+    HX_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    float *red = reinterpret_cast<float *>(&sA[0][0][0]);
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4)
+        *reinterpret_cast<f32x4 *>(red + ((wave * 4 + e4) * 64 + lane) * 4) =
+            f32x4{acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]};
+    HX_WAIT_LGKM0();
+    __builtin_amdgcn_s_barrier();
+    if (wave != 0) return;
+    f32x16 sum = f32x16{};
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const f32x4 t = *reinterpret_cast<const f32x4 *>(red + ((v * 4 + e4) * 64 + lane) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[4 * e4 + e] += t[e];
+        }
+    // lane l holds output row m0 + l % 32, columns n0 + 8 g + 4 (l / 32) .. + 3
+    const int m = m0 + r;
+    if (m >= p.M) return;
+    f16 *C = p.C;
+    const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = n0 + g * 8 + (lane >> 5) * 4;
+        float bv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
+        f16 *dst = C + (long long) m * p.ldc + n;
+        if (vec_store && n + 3 < p.N) {
+            const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = epi(sum[g * 4 + e] + bv[e], p.act, p.R, r4[e]);
+            *reinterpret_cast<f16x4 *>(dst) = o;
+        } else {
+            store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr, sum[g * 4] + bv[0],
+                       sum[g * 4 + 1] + bv[1], sum[g * 4 + 2] + bv[2], sum[g * 4 + 3] + bv[3]);
+        }
+    }
+}
+
 // ---- W^T small-M path: register operands, K split across the waves -------------
 //
 // For small M (the encoder at batch 1: M = 256) the tiled kernels leave most
@@ -1162,6 +1265,14 @@ std::atomic<int> g_ov_bm{0}, g_ov_bn{0}, g_ov_splits{0}, g_ov_path{0};
 // N or longer K are faster tiled).
 bool skinny_auto(int M, int N, int K) { return M <= 256 && N <= 1024 && K <= 1024; }
 
+// The 32x32 K-across-waves kernel: up to 256 rows and at most one round of
+// its one-per-CU workgroups (a sweep on MI355X: 256x3072x768 8.95 us vs 11.9
+// split-K, 256x768x768 4.8 vs 5.2 small-M kernel; 256x768x3072, with 768
+// tiles, 12.1 vs 8.0 tiled, and 784 or 512 rows slower too).
+bool kw_auto(int M, int N, int K) {
+    return M <= 256 && (long long) ((M + 31) / 32) * ((N + 31) / 32) <= 256 && K > 0;
+}
+
 // The rope epilogue on the direct-to-LDS kernel, one split. It is its own
 // instantiation, so it costs the plain kernels no registers; there is no
 // 256x128 rope form (its 32 unrolled rope stores push the accumulators to
@@ -1191,6 +1302,13 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     // small M: the register-operand kernel (K split across its waves, no split-K launch)
     const bool skinny_ok = MODE == B_NK && batch == 1 && p.K % BK == 0 && p.lda % 8 == 0 &&
                            p.ldb % 8 == 0 && avec && bvec && (p.M + 31) / 32 <= 65535 && !p.rcos;
+    const bool kw_ok = MODE == B_NK && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
+                       avec && bvec && (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w;
+    if (kw_ok && (path == 4 || (path == 0 && kw_auto(p.M, p.N, p.K)))) {
+        const dim3 grid((unsigned) ((p.N + 31) / 32), (unsigned) ((p.M + 31) / 32));
+        HX_LAUNCH(gemm_nk_kw, grid, dim3(TPB), 0, p);
+        return;
+    }
     if (skinny_ok && (path == 3 || (path == 0 && skinny_auto(p.M, p.N, p.K)))) {
         int bm = g_ov_bm.load(), bn = g_ov_bn.load();
         if (path != 3 || bm == 0) bm = bn = 32;
@@ -1297,7 +1415,7 @@ extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
                          (bm == 128 && bn == 128) || (bm == 64 && bn == 64) ||
                          (bm == 32 && bn == 64) || (bm == 64 && bn == 32) ||
                          (path == 3 && bm == 32 && bn == 32);
-    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 3) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 4) return HEXLIB_DSP_ERR_INVAL_PARAMS;
     g_ov_bm = bm;
     g_ov_bn = bn;
     g_ov_splits = splits;

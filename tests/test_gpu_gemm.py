@@ -214,7 +214,7 @@ def test_forced_split_batched_matmul(dev, splits):
 
 
 def test_override_rejects_bad_values(dev):
-    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 4), (256, 256, 0, 0),
+    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 5), (256, 256, 0, 0),
                  (32, 128, 0, 3), (128, 32, 0, 3)]:
         assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
     assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
@@ -464,3 +464,35 @@ def test_q8k_is_the_f16_gemm_on_its_dequantized_weight(dev):
     dev.check()
     exact = (a.astype(np.float64) @ w.astype(np.float64)).astype(np.float16)
     np.testing.assert_array_equal(dev.down(do), exact)
+
+
+@pytest.mark.parametrize("M,Kd,N,act,resid", [(256, 3072, 768, 0, True), (256, 3072, 768, 1, False),
+                                              (64, 3072, 3072, 1, False), (64, 3072, 1024, 0, False),
+                                              (70, 2048, 40, 2, True), (1, 4096, 64, 0, False),
+                                              (300, 256, 136, 0, True), (33, 512, 100, 1, False)])
+def test_kw_long_k_path(dev, M, Kd, N, act, resid):
+    """The 32x32 K-across-waves kernel (forced with path 4; automatic for
+    M <= 512 and K >= 2048): ragged M and N, every activation, with and
+    without the residual epilogue. Within the GEMM tolerance of the oracle;
+    the residual form bit-identical to the plain form followed by add_fp16."""
+    r = rng(15)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    res = h16(r.standard_normal((M, N)))
+    da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 4) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        if resid:
+            dev.lib.matmul_epilogue_f16wt_res_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr), dev.ptr(d2),
+                                                   M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    lin = dev.down(d1)
+    report(f"kw {M}x{Kd}x{N}", lin, K.matmul_epilogue_f16w(a, w, bias, act))
+    assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
+    if resid:
+        np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, lin).view(np.uint16))
