@@ -872,92 +872,164 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     }
 }
 
-// ---- W^T small-M, long-K path: 32x32 tiles, K split across the waves -----------
+// ---- W^T small-M path: K split across the waves, 256-deep stages --------------
 //
 // For few rows and a long K (fc2 at batch 1: 256x3072x768) the 64x64 tiles
 // need split-K and a second, reducing launch to fill the chip. Here a
-// 256-thread workgroup owns a 32x32 output tile (192 workgroups for fc2) and
-// walks K in KW_BK = 256-deep stages, each copied HBM->LDS by
+// 256-thread workgroup owns a T x T output tile (T = 32: 192 workgroups for
+// fc2) and walks K in KW_BK = 256-deep stages, each copied HBM->LDS by
 // global_load_lds as four 64-wide sub-slices of A and B rows (the swizzled
-// [row][64] layout of gemm_nk_lds), into a ring of KW_STAGES. Wave w multiplies
-// sub-slice w of every stage into its own 32x32 accumulator, so every LDS
-// fragment is read once per workgroup. The four partial tiles are summed
-// through LDS in wave order 0..3 (fixed, so results are identical run to run)
-// and wave 0 applies the epilogue: bias, activation, one rounding, the
-// optional residual. Requires K % KW_BK == 0 and 16-byte aligned rows.
+// [row][64] layout of gemm_nk_lds), into a small ring. Wave w multiplies
+// sub-slice w of every stage into its own accumulators for the whole tile, so
+// every LDS fragment is read once per workgroup and a K of 768 takes three
+// barriers. The four partial tiles are summed through LDS in wave order 0..3
+// (fixed, so results are identical run to run) and the epilogue applies
+// bias, activation, one rounding and the optional residual. Requires
+// K % KW_BK == 0 and 16-byte aligned rows.
 constexpr int KW_BK = 256;
-constexpr int KW_STAGES = 3;
 
+// One 32x32 output block's rope epilogue (the lane holds row m, columns
+// nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order): the same arithmetic as
+// gemm_nk_lds's rope epilogue, with every bias and table load issued first.
+__device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
+    const int half = p.rope_d >> 1;
+    const int mc = min(m, p.M - 1);
+    RopeQuad q[4];
+    bool rope[4];
+    float bv[4][4];
+    float2 c0[4], c1[4], s0[4], s1[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + (lane >> 5) * 4;
+        rope[g] = n < p.rope_cols;
+        q[g] = rope[g] ? rope_quad(n, p.rope_d) : RopeQuad{n, n + 1, 0};
+        const int f[4] = {q[g].lo, rope[g] ? q[g].hi : n + 1, q[g].lo + (rope[g] ? 1 : 2),
+                          rope[g] ? q[g].hi + 1 : n + 3};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[g][e] = (p.bias && n < p.N) ? p.bias[f[e]] : 0.0f;
+        if (rope[g]) {
+            const long long ld = p.M, o = (long long) q[g].t * ld + mc, oh = o + half * ld;
+            c0[g] = float2{p.rcos[o], p.rcos[o + ld]};
+            c1[g] = float2{p.rcos[oh], p.rcos[oh + ld]};
+            s0[g] = float2{p.rsin[o], p.rsin[o + ld]};
+            s1[g] = float2{p.rsin[oh], p.rsin[oh + ld]};
+        }
+    }
+    if (m >= p.M) return;
+    f16 *crow = p.C + (long long) m * p.ldc;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + (lane >> 5) * 4;
+        if (n >= p.N) continue;
+        if (rope[g]) {
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = apply_act(v[g * 4 + e] + bv[g][e], p.act);
+            rope_store4(crow, q[g], x, c0[g], c1[g], s0[g], s1[g]);
+        } else {
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = epi(v[g * 4 + e] + bv[g][e], p.act, false, (f16) 0);
+            *reinterpret_cast<f16x4 *>(crow + n) = o;
+        }
+    }
+}
+
+// T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
+// 2 stages -- 128 KB of LDS). With T = 64 wave w stores block w after the
+// reduction; with T = 32 wave 0 stores.
+template <int T, bool ROPE = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
-    constexpr int LOADS = 8;   // wave-instructions per stage: 4 sub-slices x (A + B)
-    static_assert(LOADS * (KW_STAGES - 1) <= 63, "vmcnt holds at most 63");
-    __shared__ __attribute__((aligned(16))) f16 sA[KW_STAGES][4][32 * DS_ROW];
-    __shared__ __attribute__((aligned(16))) f16 sB[KW_STAGES][4][32 * DS_ROW];
+    constexpr int NB = T / 32;                 // 32-row blocks per tile side
+    constexpr int STAGES = T == 32 ? 3 : 2;
+    constexpr int LOADS = 4 * 2 * (T / 32);     // wave-instructions per stage: 4 sub-slices x (A + B) x T/32
+    static_assert(LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
+    static_assert(STAGES * 4 * 2 * T * DS_ROW * 2 >= 4 * NB * NB * 16 * 64 * 4, "reduction fits in the ring");
+    __shared__ __attribute__((aligned(16))) f16 sA[STAGES][4][T * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 sB[STAGES][4][T * DS_ROW];
     const f16 *A = p.A;
     const f16 *B = reinterpret_cast<const f16 *>(p.B);
-    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int KT = p.K / KW_BK;
 
     auto issue = [&](int kt, int st) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-            lds_copy_slice<32, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
-            lds_copy_slice<32, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
+            lds_copy_slice<T, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
+            lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
-    f32x16 acc = f32x16{};
+    f32x16 acc[NB][NB];   // [column block j][row block i]
 #pragma unroll
-    for (int s = 0; s < KW_STAGES - 1; ++s)
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < NB; ++i) acc[j][i] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
         if (s < KT) issue(s, s);
     const int r = lane & 31;
     for (int kt = 0; kt < KT; ++kt) {
-        const int st = kt % KW_STAGES;
+        const int st = kt % STAGES;
         // stage kt's copies are done (this wave) once at most the later ones remain
-        if (kt + KW_STAGES - 1 <= KT) HX_WAIT_VMCNT(LOADS * (KW_STAGES - 2));
+        if (kt + STAGES - 1 <= KT) HX_WAIT_VMCNT(LOADS * (STAGES - 2));
         else HX_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();   // and every wave's; stage kt - 1's reads are done
-        if (kt + KW_STAGES - 1 < KT) issue(kt + KW_STAGES - 1, (kt + KW_STAGES - 1) % KW_STAGES);
+        if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         const f16 *as = sA[st][wave], *bs = sB[st][wave];
-        f16x8 wf[BK / 16], xf[BK / 16];
 #pragma unroll
         for (int q = 0; q < BK / 16; ++q) {
             const int c = 2 * q + (lane >> 5);
-            wf[q] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
-            xf[q] = *reinterpret_cast<const f16x8 *>(as + r * DS_ROW + ((c ^ swz(r)) << 3));
-        }
-        __builtin_amdgcn_sched_barrier(0);
+            f16x8 wf[NB], xf[NB];
 #pragma unroll
-        for (int q = 0; q < BK / 16; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[q], xf[q], acc, 0, 0, 0);
+            for (int h = 0; h < NB; ++h) {
+                const int rr = h * 32 + r;
+                wf[h] = *reinterpret_cast<const f16x8 *>(bs + rr * DS_ROW + ((c ^ swz(rr)) << 3));
+                xf[h] = *reinterpret_cast<const f16x8 *>(as + rr * DS_ROW + ((c ^ swz(rr)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int i = 0; i < NB; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+        }
     }
-    // combine the waves' partial tiles: [wave][e/4][lane][4] floats over stage 0 of sA
+    // combine the waves' partial tiles: [wave][block][e/4][lane][4] floats over the ring
     HX_WAIT_VMCNT(0);
     __builtin_amdgcn_s_barrier();
     float *red = reinterpret_cast<float *>(&sA[0][0][0]);
 #pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4)
-        *reinterpret_cast<f32x4 *>(red + ((wave * 4 + e4) * 64 + lane) * 4) =
-            f32x4{acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]};
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4)
+                *reinterpret_cast<f32x4 *>(red + (((wave * NB * NB + i * NB + j) * 4 + e4) * 64 + lane) * 4) =
+                    f32x4{acc[j][i][4 * e4], acc[j][i][4 * e4 + 1], acc[j][i][4 * e4 + 2], acc[j][i][4 * e4 + 3]};
     HX_WAIT_LGKM0();
     __builtin_amdgcn_s_barrier();
-    if (wave != 0) return;
+    if (wave >= NB * NB) return;
+    const int blk = wave;                          // block (i, j) = (blk / NB, blk % NB)
     f32x16 sum = f32x16{};
 #pragma unroll
     for (int v = 0; v < 4; ++v)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
-            const f32x4 t = *reinterpret_cast<const f32x4 *>(red + ((v * 4 + e4) * 64 + lane) * 4);
+            const f32x4 t = *reinterpret_cast<const f32x4 *>(red + (((v * NB * NB + blk) * 4 + e4) * 64 + lane) * 4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) sum[4 * e4 + e] += t[e];
         }
-    // lane l holds output row m0 + l % 32, columns n0 + 8 g + 4 (l / 32) .. + 3
-    const int m = m0 + r;
+    // lane l holds output row l % 32 of the block, columns 8 g + 4 (l / 32) .. + 3
+    const int m = m0 + (blk / NB) * 32 + r;
+    if constexpr (ROPE) {   // the rope entry point's guarantees: N % 4, rope_d % 4, ldc == N, no residual
+        store_block_rope(p, m, n0 + (blk % NB) * 32, lane, sum);
+        return;
+    }
     if (m >= p.M) return;
     f16 *C = p.C;
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const int n = n0 + g * 8 + (lane >> 5) * 4;
+        const int n = n0 + (blk % NB) * 32 + g * 8 + (lane >> 5) * 4;
         float bv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
@@ -1265,12 +1337,15 @@ std::atomic<int> g_ov_bm{0}, g_ov_bn{0}, g_ov_splits{0}, g_ov_path{0};
 // N or longer K are faster tiled).
 bool skinny_auto(int M, int N, int K) { return M <= 256 && N <= 1024 && K <= 1024; }
 
-// The 32x32 K-across-waves kernel: up to 256 rows and at most one round of
-// its one-per-CU workgroups (a sweep on MI355X: 256x3072x768 8.95 us vs 11.9
-// split-K, 256x768x768 4.8 vs 5.2 small-M kernel; 256x768x3072, with 768
-// tiles, 12.1 vs 8.0 tiled, and 784 or 512 rows slower too).
-bool kw_auto(int M, int N, int K) {
-    return M <= 256 && (long long) ((M + 31) / 32) * ((N + 31) / 32) <= 256 && K > 0;
+// The K-across-waves kernels, when their one-per-CU workgroups fit one round
+// (a sweep on MI355X): 32x32 up to 256 rows (256x3072x768 8.8 us vs 11.8
+// split-K; 256x768x768 4.8 vs 5.2 small-M kernel), else 64x64 (256x768x3072
+// 7.1 vs 8.2 tiled; 784x3072x768 16.5 vs 18.9). Returns the tile, or 0.
+int kw_auto(int M, int N) {
+    const long long t32 = (long long) ((M + 31) / 32) * ((N + 31) / 32);
+    const long long t64 = (long long) ((M + 63) / 64) * ((N + 63) / 64);
+    if (M <= 256 && t32 <= 256) return 32;
+    return t64 <= 256 ? 64 : 0;
 }
 
 // The rope epilogue on the direct-to-LDS kernel, one split. It is its own
@@ -1303,10 +1378,20 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     const bool skinny_ok = MODE == B_NK && batch == 1 && p.K % BK == 0 && p.lda % 8 == 0 &&
                            p.ldb % 8 == 0 && avec && bvec && (p.M + 31) / 32 <= 65535 && !p.rcos;
     const bool kw_ok = MODE == B_NK && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
-                       avec && bvec && (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w;
-    if (kw_ok && (path == 4 || (path == 0 && kw_auto(p.M, p.N, p.K)))) {
+                       avec && bvec && (p.M + 31) / 32 <= 65535 && !p.ln_w;
+    int kw = 0;
+    if (kw_ok && path == 4) kw = g_ov_bm.load() == 64 ? 64 : 32;
+    else if (kw_ok && path == 0) kw = kw_auto(p.M, p.N);
+    if (kw && p.rcos) kw = 64;   // the rope epilogue exists in the 64x64 form
+    if (kw == 64) {
+        const dim3 grid((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64));
+        if (p.rcos) HX_LAUNCH((gemm_nk_kw<64, true>), grid, dim3(TPB), 0, p);
+        else HX_LAUNCH((gemm_nk_kw<64>), grid, dim3(TPB), 0, p);
+        return;
+    }
+    if (kw == 32) {
         const dim3 grid((unsigned) ((p.N + 31) / 32), (unsigned) ((p.M + 31) / 32));
-        HX_LAUNCH(gemm_nk_kw, grid, dim3(TPB), 0, p);
+        HX_LAUNCH((gemm_nk_kw<32>), grid, dim3(TPB), 0, p);
         return;
     }
     if (skinny_ok && (path == 3 || (path == 0 && skinny_auto(p.M, p.N, p.K)))) {

@@ -466,15 +466,17 @@ def test_q8k_is_the_f16_gemm_on_its_dequantized_weight(dev):
     np.testing.assert_array_equal(dev.down(do), exact)
 
 
+@pytest.mark.parametrize("tile", [32, 64])
 @pytest.mark.parametrize("M,Kd,N,act,resid", [(256, 3072, 768, 0, True), (256, 3072, 768, 1, False),
                                               (64, 3072, 3072, 1, False), (64, 3072, 1024, 0, False),
                                               (70, 2048, 40, 2, True), (1, 4096, 64, 0, False),
                                               (300, 256, 136, 0, True), (33, 512, 100, 1, False)])
-def test_kw_long_k_path(dev, M, Kd, N, act, resid):
-    """The 32x32 K-across-waves kernel (forced with path 4; automatic for
-    M <= 512 and K >= 2048): ragged M and N, every activation, with and
-    without the residual epilogue. Within the GEMM tolerance of the oracle;
-    the residual form bit-identical to the plain form followed by add_fp16."""
+def test_kw_long_k_path(dev, tile, M, Kd, N, act, resid):
+    """The K-across-waves kernels (32x32 and 64x64 tiles, forced with path 4;
+    automatic where their workgroups fit one round): ragged M and N, every
+    activation, with and without the residual epilogue. Within the GEMM
+    tolerance of the oracle; the residual form bit-identical to the plain form
+    followed by add_fp16."""
     r = rng(15)
     a = h16(r.standard_normal((M, Kd)))
     w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
@@ -482,7 +484,7 @@ def test_kw_long_k_path(dev, M, Kd, N, act, resid):
     res = h16(r.standard_normal((M, N)))
     da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
     d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
-    assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 4) == 1
+    assert dev.lib.hexlib_gpu_gemm_override(tile if tile == 64 else 0, tile if tile == 64 else 0, 0, 4) == 1
     try:
         dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
         if resid:
@@ -492,7 +494,37 @@ def test_kw_long_k_path(dev, M, Kd, N, act, resid):
     finally:
         dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
     lin = dev.down(d1)
-    report(f"kw {M}x{Kd}x{N}", lin, K.matmul_epilogue_f16w(a, w, bias, act))
+    report(f"kw{tile} {M}x{Kd}x{N}", lin, K.matmul_epilogue_f16w(a, w, bias, act))
     assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
     if resid:
         np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, lin).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,Kd,heads,d,extra", [(256, 768, 12, 64, 768), (200, 512, 3, 16, 32), (70, 256, 2, 64, 128)])
+def test_kw64_rope_epilogue(dev, M, Kd, heads, d, extra):
+    """The 64x64 K-across-waves kernel with the rope epilogue (the encoder's
+    q/k/v linear at batch 1) is bit-identical to the same kernel's plain
+    output followed by rope_2d on the q and k heads."""
+    r = rng(22)
+    N = 2 * heads * d + extra
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    cos, sin = _rope_tables(r, M, d)
+    da, db = dev.up(a), dev.up(bias)
+    dc, ds = dev.up(np.ascontiguousarray(cos.T)), dev.up(np.ascontiguousarray(sin.T))
+    dw, dwr = dev.up(np.ascontiguousarray(w.T)), dev.up(K.permute_rope_rows(w.T, heads, d))
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(64, 64, 0, 4) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, 0)
+        dev.lib.matmul_epilogue_f16wt_rope_fp16(dev.ptr(da), dev.ptr(dwr), dev.ptr(db), dev.ptr(dc), dev.ptr(ds),
+                                                dev.ptr(d2), M, Kd, N, 0, heads, d)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    lin, got = dev.down(d1), dev.down(d2)
+    want = lin.copy()
+    want[:, :2 * heads * d] = K.rope_2d_fp16(lin[:, :2 * heads * d].reshape(M, 2 * heads, d), cos, sin).reshape(M, -1)
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+    assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, 0), 1e-2, 1e-3).all()
