@@ -1047,6 +1047,233 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     }
 }
 
+// ---- W^T large-M path: big wave tiles, fragment reads under the MFMAs ----------
+//
+// For many rows (the encoder at batch 32: M = 8192) the tiled kernel's waves
+// are bound by LDS fragment reads and their latency, not by the MFMAs: a wave
+// reads TM + TN fragments per 16-deep k step for TM x TN MFMAs and, one wave
+// per SIMD, waits for them before it multiplies. Here each of the 4 waves
+// (2 x 2) owns a (BM / 2) x (BN / 2) sub-tile -- 128 x 128 in the 256 x 256
+// tile -- and step q + 1's fragments are read while step q's MFMAs run: two
+// register sets, the reads interleaved one by one between the MFMAs. The K ring
+// is gemm_nk_lds's direct-to-LDS ring (64-wide slices, STAGES deep); its one
+// barrier per slice sits before the slice's last k step, whose MFMAs then
+// cover the next slice's first reads. Workgroups are renumbered so that each
+// XCD (the hardware deals workgroup b to XCD b % 8) takes one contiguous run of
+// the row-major tile order, so the workgroups sharing an A row block share one
+// L2. One batch, no split: K % 64 == 0, 16-byte aligned rows.
+constexpr int XCDS = 8;
+
+// Scheduling groups for one k step: an LDS read, then NM / NR MFMAs, NR
+// times (the last group takes the remaining MFMAs).
+template <int G, int NR, int NM>
+__device__ __forceinline__ void interleave_reads() {
+    if constexpr (G < NR) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, G < NR - 1 ? NM / NR : NM - (NR - 1) * (NM / NR), 0);
+        interleave_reads<G + 1, NR, NM>();
+    }
+}
+
+template <int BM, int BN, int STAGES, bool ROPE = false>
+__global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntiles) {
+    constexpr int NW = 4, WN = 2;
+    constexpr int TM = BM / 64, TN = BN / 64;     // 32x32 blocks per wave
+    constexpr int LOADS = (BM + BN) / (8 * NW);    // wave-instructions per ring slice
+    constexpr int NR = TM + TN, NM = TM * TN;      // fragment reads and MFMAs per k step
+    static_assert(STAGES >= 2 && LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
+    // one buffer: the A ring, then the B ring; the epilogue reuses all of it
+    __shared__ __attribute__((aligned(16))) f16 lds[STAGES * (BM + BN) * DS_ROW];
+    auto sA = [&](int st) { return lds + st * (BM * DS_ROW); };
+    auto sB = [&](int st) { return lds + STAGES * (BM * DS_ROW) + st * (BN * DS_ROW); };
+
+    // XCD-contiguous numbering: a bijection of [0, ntiles) whatever the dealing
+    const int b = blockIdx.x, q8 = ntiles / XCDS, r8 = ntiles % XCDS, x = b % XCDS, l = b / XCDS;
+    const int t = (x < r8 ? x * (q8 + 1) : r8 * (q8 + 1) + (x - r8) * q8) + l;
+    const int m0 = (t / gx) * BM, n0 = (t % gx) * BN;
+    const f16 *A = p.A;
+    const f16 *B = reinterpret_cast<const f16 *>(p.B);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave / WN) * (BM / 2), wn = (wave % WN) * (BN / 2);
+    const int KT = p.K / BK;
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
+
+    struct Frags {
+        f16x8 w[TN], x[TM];
+    };
+    auto issue = [&](int kt, int st) {
+        lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kt * BK, sA(st));
+        lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kt * BK, sB(st));
+    };
+    // every row this lane reads has the same swizzle: wm, wn and 32 j are multiples of 16
+    const int r = lane & 31, sw = swz(r);
+    auto read = [&](int st, int q, Frags &f) {
+        const int c = (2 * q + (lane >> 5)) ^ sw;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            f.w[j] = *reinterpret_cast<const f16x8 *>(sB(st) + (wn + j * 32 + r) * DS_ROW + (c << 3));
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            f.x[i] = *reinterpret_cast<const f16x8 *>(sA(st) + (wm + i * 32 + r) * DS_ROW + (c << 3));
+    };
+    // step q's MFMAs with step q + 1's reads dealt between them, reads first
+    auto step = [&](const Frags &cur, Frags &nxt, int st, int q) {
+        read(st, q, nxt);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.w[j], cur.x[i], acc[j][i], 0, 0, 0);
+        interleave_reads<0, NR, NM>();
+    };
+
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+        if (s < KT) issue(s, s);
+    if (KT >= STAGES) HX_WAIT_VMCNT(LOADS * (STAGES - 1));
+    else HX_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    Frags f0, f1;
+    read(0, 0, f0);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int st = kt % STAGES;
+        step(f0, f1, st, 1);
+        step(f1, f0, st, 2);
+        step(f0, f1, st, 3);
+        if (kt + 1 < KT) {
+            // this wave's reads of slot st are done, and (after the barrier) every
+            // wave's; slice kt + 1 has landed once at most the later slices remain
+            HX_WAIT_LGKM0();
+            if (kt + STAGES <= KT) HX_WAIT_VMCNT(LOADS * (STAGES - 2));
+            else HX_WAIT_VMCNT(0);
+            __builtin_amdgcn_s_barrier();
+            if (kt + STAGES < KT) issue(kt + STAGES, st);
+        }
+        // the last slice's reads here fetch a stale slot and are never used: one
+        // MFMA path through the loop keeps the accumulators in place
+        step(f1, f0, (kt + 1) % STAGES, 0);
+    }
+
+    // Epilogue through LDS (the ring is free now), one 32-row block of every
+    // wave at a time: the waves write their fp32 blocks, then each thread takes
+    // a fixed 8-column chunk of every RPI-th staged row -- bias (loaded once),
+    // activation, rounding, the optional residual (prefetched one row ahead),
+    // one 16-byte store. The rows are padded by 4 floats so the 32 rows of a
+    // block's writes fall in distinct banks. The host guarantees N % 8 == 0,
+    // ldc % 8 == 0 and 16-byte aligned C, R and bias.
+    constexpr int EROW = BN + 4;                   // floats per staged row
+    constexpr int CPR = BN / 8, RPI = TPB / CPR;  // chunks per row, rows per sweep
+    static_assert(2 * 32 * EROW * 4 <= STAGES * (BM + BN) * DS_ROW * 2, "a staged row pair fits the ring");
+    float *stage = reinterpret_cast<float *>(lds);
+    const int tid = threadIdx.x, c8 = (tid % CPR) * 8, sr0 = tid / CPR, n = n0 + c8;
+    const bool cols = tid < RPI * CPR && n < p.N;
+    // Rope (the rope entry point's guarantees plus rope_d % 8 == 0 and no
+    // residual): a chunk of 8 computed columns lies in one rope head or wholly
+    // past them, and holds two pair-interleaved quads (see rope_store4).
+    const bool rope = ROPE && cols && n < p.rope_cols;
+    const RopeQuad q0 = rope ? rope_quad(n, p.rope_d) : RopeQuad{}, q1 = rope ? rope_quad(n + 4, p.rope_d) : RopeQuad{};
+    // bias by computed column: a rope quad's columns are features lo, hi, lo + 1, hi + 1
+    f32x4 b0 = {}, b1 = {};
+    if (p.bias && rope) {
+        b0 = f32x4{p.bias[q0.lo], p.bias[q0.hi], p.bias[q0.lo + 1], p.bias[q0.hi + 1]};
+        b1 = f32x4{p.bias[q1.lo], p.bias[q1.hi], p.bias[q1.lo + 1], p.bias[q1.hi + 1]};
+    } else if (p.bias && cols) {
+        b0 = *reinterpret_cast<const f32x4 *>(p.bias + n);
+        b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
+    }
+    HX_WAIT_VMCNT(0);
+    f16 *C = p.C;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        __builtin_amdgcn_s_barrier();              // the ring's (or the last pass's) reads are done
+        const int srow = (wave / WN) * 32 + r;     // staged row: 32 rows per wave row
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<f32x4 *>(stage + srow * EROW + wn + j * 32 + g * 8 + (lane >> 5) * 4) =
+                    f32x4{acc[j][i][g * 4], acc[j][i][g * 4 + 1], acc[j][i][g * 4 + 2], acc[j][i][g * 4 + 3]};
+        HX_WAIT_LGKM0();
+        __builtin_amdgcn_s_barrier();
+        if (!cols) continue;
+        // staged rows 0..31 are block i of wave row 0, 32..63 of wave row 1
+        auto row_of = [&](int sr) { return m0 + (sr >> 5) * (BM / 2) + i * 32 + (sr & 31); };
+        if constexpr (ROPE) {
+            if (rope) {
+                // the two quads' tables for row m: quad 0 uses table rows t0, t0 + 1 and
+                // their partners half further; quad 1 the next two
+                const int half = p.rope_d >> 1;
+                const long long ld = p.M;
+                struct Tab {
+                    float c[8], s[8];
+                };
+                auto tabs = [&](int sr) {
+                    Tab t{};
+                    const int m = row_of(sr);
+                    if (sr < 64 && m < p.M) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const long long o = (long long) (q0.t + u) * ld + m, oh = o + half * ld;
+                            t.c[u] = p.rcos[o];
+                            t.c[4 + u] = p.rcos[oh];
+                            t.s[u] = p.rsin[o];
+                            t.s[4 + u] = p.rsin[oh];
+                        }
+                    }
+                    return t;
+                };
+                Tab tn = tabs(sr0);
+                for (int sr = sr0; sr < 64; sr += RPI) {
+                    const Tab t = tn;
+                    tn = tabs(sr + RPI);
+                    const int m = row_of(sr);
+                    if (m >= p.M) continue;
+                    const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
+                    const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
+                    float x0[4], x1[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x0[e] = apply_act(v0[e] + b0[e], p.act);
+                        x1[e] = apply_act(v1[e] + b1[e], p.act);
+                    }
+                    f16 *crow = C + (long long) m * p.ldc;
+                    rope_store4(crow, q0, x0, float2{t.c[0], t.c[1]}, float2{t.c[4], t.c[5]},
+                                float2{t.s[0], t.s[1]}, float2{t.s[4], t.s[5]});
+                    rope_store4(crow, q1, x1, float2{t.c[2], t.c[3]}, float2{t.c[6], t.c[7]},
+                                float2{t.s[2], t.s[3]}, float2{t.s[6], t.s[7]});
+                }
+                continue;
+            }
+        }
+        auto resid = [&](int sr) {
+            const int m = row_of(sr);
+            return p.R && sr < 64 && m < p.M ? *reinterpret_cast<const f16x8 *>(p.R + (long long) m * p.ldr + n)
+                                             : f16x8{};
+        };
+        f16x8 rn = resid(sr0);
+        for (int sr = sr0; sr < 64; sr += RPI) {
+            const f16x8 r8 = rn;
+            rn = resid(sr + RPI);
+            const int m = row_of(sr);
+            if (m >= p.M) continue;
+            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
+            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
+            f16x8 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                o[e] = epi(v0[e] + b0[e], p.act, p.R, r8[e]);
+                o[e + 4] = epi(v1[e] + b1[e], p.act, p.R, r8[e + 4]);
+            }
+            *reinterpret_cast<f16x8 *>(C + (long long) m * p.ldc + n) = o;
+        }
+    }
+}
+
 // ---- W^T small-M path: register operands, K split across the waves -------------
 //
 // For small M (the encoder at batch 1: M = 256) the tiled kernels leave most
@@ -1348,6 +1575,54 @@ int kw_auto(int M, int N) {
     return t64 <= 256 ? 64 : 0;
 }
 
+// The large-tile kernel for tile bm x bn with a ring of `stages` slices;
+// false when that form is not built (the rope epilogue exists for the forms
+// the automatic choice uses).
+bool launch_big(const GemmArgs &p, Tile t, int stages) {
+    const int gx = (p.N + t.bn - 1) / t.bn, gy = (p.M + t.bm - 1) / t.bm;
+    const long long nt = (long long) gx * gy;
+    if (nt > 0x7fffffffLL) return false;
+    const dim3 grid((unsigned) nt), block(TPB);
+    const int n = (int) nt;
+#define HX_BIG(BM_, BN_, S_)                                                              \
+    if (t.bm == BM_ && t.bn == BN_ && stages == S_) {                                     \
+        if (p.rcos) return false;                                                         \
+        HX_LAUNCH((gemm_nk_big<BM_, BN_, S_>), grid, block, 0, p, gx, n);                 \
+        return true;                                                                      \
+    }
+#define HX_BIG_ROPE(BM_, BN_, S_)                                                         \
+    if (t.bm == BM_ && t.bn == BN_ && stages == S_) {                                     \
+        if (p.rcos) HX_LAUNCH((gemm_nk_big<BM_, BN_, S_, true>), grid, block, 0, p, gx, n); \
+        else HX_LAUNCH((gemm_nk_big<BM_, BN_, S_>), grid, block, 0, p, gx, n);            \
+        return true;                                                                      \
+    }
+    HX_BIG(256, 256, 2)
+    HX_BIG(256, 192, 2)
+    HX_BIG(128, 256, 2)
+    HX_BIG(128, 256, 3)
+    HX_BIG_ROPE(128, 192, 2)
+    HX_BIG(128, 192, 3)
+    HX_BIG(256, 128, 2)
+    HX_BIG(256, 128, 3)
+    HX_BIG_ROPE(128, 128, 2)
+    HX_BIG(128, 128, 3)
+#undef HX_BIG
+#undef HX_BIG_ROPE
+    return false;
+}
+
+// The large-tile kernel's tile for an M x N product, or {0, 0} for the other
+// paths. From a sweep of every form on MI355X: the 128 x 128 tile with a
+// 2-slice ring (64 KB of LDS, two workgroups per CU) is the fastest form on
+// the encoder's batch-32 shapes -- 8192 x 768 x 3072 81 us against 96 us,
+// 8192 x 3072 x 768 59 against 74, 8192 x 768 x 768 28 against 33 -- wherever
+// its grid fills at least one round of 256 workgroups; with fewer tiles
+// (784 rows, 2048 x 3072 x 1024) the other paths are faster.
+Tile big_auto(int M, int N) {
+    const long long tiles = (long long) ((M + 127) / 128) * ((N + 127) / 128);
+    return tiles >= 256 ? Tile{128, 128} : Tile{0, 0};
+}
+
 // The rope epilogue on the direct-to-LDS kernel, one split. It is its own
 // instantiation, so it costs the plain kernels no registers; there is no
 // 256x128 rope form (its 32 unrolled rope stores push the accumulators to
@@ -1379,6 +1654,18 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
                            p.ldb % 8 == 0 && avec && bvec && (p.M + 31) / 32 <= 65535 && !p.rcos;
     const bool kw_ok = MODE == B_NK && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                        avec && bvec && (p.M + 31) / 32 <= 65535 && !p.ln_w;
+    // the large-tile kernel: its epilogue stores 8-column chunks (and, with the
+    // rope, needs whole rope heads of 8-column chunks and no residual)
+    const bool big_ok = MODE == B_NK && batch == 1 && p.K % BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
+                        avec && bvec && !p.ln_w && p.N % 8 == 0 && p.ldc % 8 == 0 &&
+                        ((uintptr_t) p.C & 15) == 0 && (!p.bias || ((uintptr_t) p.bias & 15) == 0) &&
+                        (!p.R || (p.ldr % 8 == 0 && ((uintptr_t) p.R & 15) == 0)) &&
+                        (!p.rcos || (p.rope_d % 8 == 0 && p.rope_cols % 8 == 0 && !p.R));
+    if (big_ok && (path == 5 || path == 0)) {
+        const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N);
+        const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;
+        if (bt.bm && launch_big(p, bt, stages)) return;
+    }
     int kw = 0;
     if (kw_ok && path == 4) kw = g_ov_bm.load() == 64 ? 64 : 32;
     else if (kw_ok && path == 0) kw = kw_auto(p.M, p.N);
@@ -1407,9 +1694,11 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     Tile t;
     int splits;
     plan_tiles(p.M, p.N, p.K, batch, t, splits);
-    if (const int bm = g_ov_bm.load()) t = {bm, g_ov_bn.load()};
+    // path 5's tile and ring depth belong to the large-tile kernel: a shape it
+    // cannot take runs with the heuristic's choice
+    if (const int bm = g_ov_bm.load(); bm && path != 5) t = {bm, g_ov_bn.load()};
     if (t.bm == 32 && t.bn == 32) t = {64, 64};   // the skinny-only tile, on a shape it cannot take
-    if (const int s = g_ov_splits.load()) splits = s;
+    if (const int s = g_ov_splits.load(); s && path != 5) splits = s;
     if (splits > 1) {
         const int kt = (p.K + BK - 1) / BK;
         const int per = (kt + splits - 1) / splits;
@@ -1496,11 +1785,14 @@ int prepare_workspace() {
 }  // namespace hx
 
 extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
-    const bool tile_ok = (bm == 0 && bn == 0) || (bm == 256 && bn == 128) ||
-                         (bm == 128 && bn == 128) || (bm == 64 && bn == 64) ||
-                         (bm == 32 && bn == 64) || (bm == 64 && bn == 32) ||
-                         (path == 3 && bm == 32 && bn == 32);
-    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 4) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+    const bool tile_ok = path == 5 ? (bm == 128 || bm == 256) && (bn == 128 || bn == 192 || bn == 256)
+                                   : (bm == 0 && bn == 0) || (bm == 256 && bn == 128) ||
+                                         (bm == 128 && bn == 128) || (bm == 64 && bn == 64) ||
+                                         (bm == 32 && bn == 64) || (bm == 64 && bn == 32) ||
+                                         (path == 3 && bm == 32 && bn == 32);
+    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 5 ||
+        (path == 5 && splits > 3))
+        return HEXLIB_DSP_ERR_INVAL_PARAMS;
     g_ov_bm = bm;
     g_ov_bn = bn;
     g_ov_splits = splits;

@@ -311,9 +311,12 @@ const char *hexlib_gpu_status_name(int status);
  * bm x bn (256x128, 128x128, 64x64, 32x64, 64x32; 0x0 = heuristic), split-K count
  * (0 = heuristic, at most 16) and W^T code path (0 = automatic,
  * 1 = register-staged, 2 = direct-to-LDS, 3 = the small-M register-operand
- * kernel with tile 32x32 or 32x64, 4 = the 32x32 K-across-waves kernel for
- * K % 256 == 0; 2, 3 and 4 apply where their preconditions hold). Returns
- * HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
+ * kernel with tile 32x32 or 32x64, 4 = the K-across-waves kernel for
+ * K % 256 == 0 (tile 64x64 selects its 64x64 form, else 32x32), 5 = the
+ * large-tile kernel with bm in {128, 256} and bn in {128, 192, 256}, where
+ * `splits` is its ring depth instead (0 = 2, at most 3; a form not built falls
+ * back to the automatic choice); 2 to 5 apply where their preconditions
+ * hold). Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
 int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path);
 /* sizeof of each wire struct, in declaration order above (batch_hdr, buf_desc,
  * tensor, op_desc, rsp_hdr, op_result, hexlib_args); returns the count. */

@@ -214,8 +214,8 @@ def test_forced_split_batched_matmul(dev, splits):
 
 
 def test_override_rejects_bad_values(dev):
-    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 5), (256, 256, 0, 0),
-                 (32, 128, 0, 3), (128, 32, 0, 3)]:
+    for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 6), (256, 256, 0, 0),
+                 (32, 128, 0, 3), (128, 32, 0, 3), (64, 64, 0, 5), (256, 256, 4, 5), (192, 256, 0, 5)]:
         assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
     assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
 
@@ -528,3 +528,77 @@ def test_kw64_rope_epilogue(dev, M, Kd, heads, d, extra):
     want[:, :2 * heads * d] = K.rope_2d_fp16(lin[:, :2 * heads * d].reshape(M, 2 * heads, d), cos, sin).reshape(M, -1)
     np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
     assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, 0), 1e-2, 1e-3).all()
+
+
+BIG_FORMS = [(256, 256, 2), (256, 192, 2), (128, 256, 2), (128, 256, 3), (128, 192, 2), (128, 192, 3),
+             (256, 128, 2), (256, 128, 3), (128, 128, 2), (128, 128, 3)]
+
+
+@pytest.mark.parametrize("form", BIG_FORMS)
+@pytest.mark.parametrize("M,Kd,N,act,resid", [(300, 256, 136, 1, True), (520, 1024, 392, 2, False),
+                                              (1100, 768, 776, 0, True), (64, 64, 8, 1, False)])
+def test_big_tile_path(dev, form, M, Kd, N, act, resid):
+    """The large-tile kernel (path 5), every built tile and ring depth: ragged M
+    and N (N % 8 == 0, down to one 8-column group), K from one slice, every
+    activation, with and without the residual epilogue. Bit-identical to the
+    direct-to-LDS 64x64 kernel without split-K (the same per-output MFMA
+    accumulation order), within the GEMM tolerance of the oracle, and the
+    residual form bit-identical to the plain form followed by add_fp16."""
+    bm, bn, stages = form
+    r = rng(16)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    res = h16(r.standard_normal((M, N)))
+    da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
+    d0, d1, d2 = (dev.empty((M, N), np.float16) for _ in range(3))
+    assert dev.lib.hexlib_gpu_gemm_override(64, 64, 1, 2) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d0), M, Kd, N, act)
+        assert dev.lib.hexlib_gpu_gemm_override(bm, bn, stages, 5) == 1
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        if resid:
+            dev.lib.matmul_epilogue_f16wt_res_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr), dev.ptr(d2),
+                                                   M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    lin = dev.down(d1)
+    np.testing.assert_array_equal(lin.view(np.uint16), dev.down(d0).view(np.uint16))
+    assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
+    if resid:
+        np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, lin).view(np.uint16))
+
+
+@pytest.mark.parametrize("form", [(128, 128, 2), (128, 192, 2), None])
+@pytest.mark.parametrize("M,Kd,heads,d,extra,act", [(1100, 768, 12, 64, 768, 0), (300, 256, 3, 16, 64, 1),
+                                                    (520, 512, 4, 32, 128, 2), (2048, 768, 12, 64, 768, 0)])
+def test_big_tile_rope_epilogue(dev, form, M, Kd, heads, d, extra, act):
+    """The large-tile kernel's rope epilogue (forced with path 5, or the
+    automatic choice where the grid fills a round: form None) is bit-identical
+    to the same kernel's plain output followed by rope_2d on the q and k
+    heads; ragged M, head widths 16 to 64, every activation."""
+    r = rng(23)
+    N = 2 * heads * d + extra
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    cos, sin = _rope_tables(r, M, d)
+    da, db = dev.up(a), dev.up(bias)
+    dc, ds = dev.up(np.ascontiguousarray(cos.T)), dev.up(np.ascontiguousarray(sin.T))
+    dw, dwr = dev.up(np.ascontiguousarray(w.T)), dev.up(K.permute_rope_rows(w.T, heads, d))
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    if form:
+        assert dev.lib.hexlib_gpu_gemm_override(form[0], form[1], form[2], 5) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        dev.lib.matmul_epilogue_f16wt_rope_fp16(dev.ptr(da), dev.ptr(dwr), dev.ptr(db), dev.ptr(dc), dev.ptr(ds),
+                                                dev.ptr(d2), M, Kd, N, act, heads, d)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    lin, got = dev.down(d1), dev.down(d2)
+    want = lin.copy()
+    want[:, :2 * heads * d] = K.rope_2d_fp16(lin[:, :2 * heads * d].reshape(M, 2 * heads, d), cos, sin).reshape(M, -1)
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+    assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
