@@ -56,9 +56,15 @@ __device__ __forceinline__ float f32_rounded(float v) {
 }
 
 // tanh-form GELU (ACT2FN["gelu_pytorch_tanh"]) and exact erf GELU, in fp32.
+// GELU, tanh form: 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3).
+// Since 1 + tanh(u) = 2 / (1 + exp(-2u)), this is x / (1 + exp(-2u)): one
+// hardware exp2 and one reciprocal instead of a library tanh (a few fp32 ulps
+// from the tanh form, far below the fp16 rounding of every consumer). Large
+// negative x sends exp(-2u) to +inf and the result to -0; large positive x
+// sends it to 0 and the result to x.
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-    const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.0f + tanhf(inner));
+    const float m2u = -1.5957691216057308f * (x + 0.044715f * x * x * x);   // -2u
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m2u * 1.4426950408889634f));
 }
 
 __device__ __forceinline__ float gelu_erf_f32(float x) {
