@@ -31,10 +31,13 @@
 //                 16 probabilities, provided A's k index means the same key.
 // To make that true the K rows are loaded in a permuted key order: S^T row r
 // holds key kperm(r), chosen so that P's k index 8h + j of chunk c is key
-// 16c + 8h + j; the V^T operand then reads 8 consecutive keys. V^T is formed
-// through a wave-private LDS tile ([D][40] halves, 80-byte rows: the 16 rows
-// one ds_read_b128 phase touches fall in 16 distinct bank groups). LDS
-// operations of one wave complete in order, so the wave-private tile needs no
+// 16c + 8h + j; the V^T operand then needs 8 consecutive keys of one d. The V
+// tile goes to a wave-private LDS tile as loaded ([key][d], 16-byte writes,
+// 192-byte rows) and each V^T operand is two ds_read_b64_tr_b16: within each
+// 16-lane group, lane 4a + b receives element b of the 8 bytes that lanes a,
+// a + 4, a + 8, a + 12 address, so lanes addressing 4 consecutive d of 4
+// consecutive keys deliver to each lane 4 keys of one d. LDS operations of one
+// wave complete in order, so the wave-private tile needs no
 // barrier; the only workgroup barrier is before the merge, which every wave
 // reaches.
 #include <cmath>
@@ -44,9 +47,16 @@
 
 namespace {
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+
 constexpr int QT = 32;          // queries per wave
 constexpr int KT = 32;          // keys per tile
-constexpr int VT_STRIDE = 40;   // halves per LDS row of V^T
+// halves per LDS row of the V tile: the 4 rows x 64 bytes a 32-lane
+// transpose-read phase touches fall in 4 distinct 16-bank windows (192-byte
+// rows for D = 64; D = 32 rows are 64 bytes and need no padding)
+template <int D>
+constexpr int v_stride() { return D == 64 ? 96 : D; }
 constexpr int CUS = 256;        // MI355X compute units
 
 __device__ __forceinline__ int kperm(int r) {
@@ -87,7 +97,8 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     constexpr int KC = D / 16;   // 16-wide d chunks of q.k
     constexpr int DT = D / 32;   // 32-row tiles of O^T
     constexpr int VCH = D / 8;   // 16-byte chunks per V row
-    __shared__ __attribute__((aligned(16))) f16 vt_all[WAVES][D * VT_STRIDE];
+    constexpr int V_STRIDE = v_stride<D>();
+    __shared__ __attribute__((aligned(16))) f16 v_all[WAVES][KT * V_STRIDE];
     __shared__ float part_o[WAVES][QT][D + 1];
     __shared__ float part_m[WAVES][QT], part_l[WAVES][QT];
 
@@ -100,7 +111,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     f16 *ob = o + row0 * ldo + (long long) h * D;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
     const int q0 = blockIdx.x * QT;
-    f16 *vt = vt_all[wave];
+    f16 *vt = v_all[wave];
+    // transpose-read addresses (halves) within the tile: key 8 hl + 4 u + s / 4,
+    // d 16 ((lane / 16) % 2) + 4 (s % 4), s = lane % 16; chunk c adds 16 keys, d tile t 32 d
+    const int tr_off = (8 * hl + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     // B operand of S^T: query column c32, d = 16 kk + 8 hl .. +8
     f16x8 qf[KC];
@@ -124,13 +138,11 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
         const int kn = kt + WAVES * KT;
         if (kn < T) load_tile<D>(kb, ldqk, vb, ldv, T, kn, krow_key, lane, nxt);
 
-        // V tile -> wave-private LDS as V^T[d][key]
+        // V tile -> wave-private LDS as loaded, [key][d]
 #pragma unroll
         for (int i = 0; i < D / 16; ++i) {
             const int e = lane + 64 * i;
-            const int vk = e / VCH, d0 = (e % VCH) * 8;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) vt[(d0 + j) * VT_STRIDE + vk] = cur.v[i][j];
+            *reinterpret_cast<f16x8 *>(vt + (e / VCH) * V_STRIDE + (e % VCH) * 8) = cur.v[i];
         }
 
         f32x16 s = f32x16{};
@@ -167,7 +179,13 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
-                const f16x8 va = *reinterpret_cast<const f16x8 *>(vt + (t * 32 + c32) * VT_STRIDE + 16 * c + 8 * hl);
+                // V^T rows d = 32 t + lane % 32, keys 16 c + 8 hl .. + 8
+                const f16 *base = vt + tr_off + 16 * c * V_STRIDE + 32 * t;
+                const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4i16 *) (base));
+                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4i16 *) (base + 4 * V_STRIDE));
+                const f16x8 va = __builtin_bit_cast(f16x8, (v8i16){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
                 oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], oacc[t], 0, 0, 0);
             }
         cur = nxt;
