@@ -1064,13 +1064,14 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 // L2. One batch, no split: K % 64 == 0, 16-byte aligned rows.
 constexpr int XCDS = 8;
 
-// Scheduling groups for one k step: an LDS read, then NM / NR MFMAs, NR
-// times (the last group takes the remaining MFMAs).
+// Scheduling groups for one k step: an LDS read then an MFMA, NR times, then
+// the step's remaining NM - NR MFMAs -- the reads go out early in the step.
 template <int G, int NR, int NM>
 __device__ __forceinline__ void interleave_reads() {
+    static_assert(NM >= NR, "at least one MFMA per read");
     if constexpr (G < NR) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, G < NR - 1 ? NM / NR : NM - (NR - 1) * (NM / NR), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, G < NR - 1 ? 1 : NM - (NR - 1), 0);
         interleave_reads<G + 1, NR, NM>();
     }
 }
@@ -1121,7 +1122,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         for (int i = 0; i < TM; ++i)
             f.x[i] = *reinterpret_cast<const f16x8 *>(sA(st) + (wm + i * 32 + r) * DS_ROW + (c << 3));
     };
-    // step q's MFMAs with step q + 1's reads dealt between them, reads first
+    // one k step's MFMAs (from cur) with a later step's reads (into nxt) dealt between them
     auto step = [&](const Frags &cur, Frags &nxt, int st, int q) {
         read(st, q, nxt);
 #pragma unroll
@@ -1138,13 +1139,18 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     if (KT >= STAGES) HX_WAIT_VMCNT(LOADS * (STAGES - 1));
     else HX_WAIT_VMCNT(0);
     __builtin_amdgcn_s_barrier();
-    Frags f0, f1;
+    // Fragments are read two k steps ahead (four register sets): step q's
+    // MFMAs run while step q + 2's fragments arrive. The slice's barrier sits
+    // after step 1, once this wave's reads of the slot (steps 2 and 3, issued
+    // during steps 0 and 1) are done; steps 2 and 3 then read the next slice's
+    // steps 0 and 1.
+    Frags f0, f1, f2, f3;
     read(0, 0, f0);
+    read(0, 1, f1);
     for (int kt = 0; kt < KT; ++kt) {
         const int st = kt % STAGES;
-        step(f0, f1, st, 1);
-        step(f1, f0, st, 2);
-        step(f0, f1, st, 3);
+        step(f0, f2, st, 2);
+        step(f1, f3, st, 3);
         if (kt + 1 < KT) {
             // this wave's reads of slot st are done, and (after the barrier) every
             // wave's; slice kt + 1 has landed once at most the later slices remain
@@ -1156,7 +1162,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         }
         // the last slice's reads here fetch a stale slot and are never used: one
         // MFMA path through the loop keeps the accumulators in place
-        step(f1, f0, (kt + 1) % STAGES, 0);
+        step(f2, f0, (kt + 1) % STAGES, 0);
+        step(f3, f1, (kt + 1) % STAGES, 1);
     }
 
     // Epilogue through LDS (the ring is free now), one 32-row block of every
