@@ -1115,6 +1115,27 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     const int wm = (wave / WN) * (BM / 2), wn = (wave % WN) * (BN / 2);
     const int KT = p.K / BK;
 
+    // The epilogue's column chunk and bias (see below), loaded before the K loop.
+    constexpr int EROW = BN + 4;                   // floats per staged row
+    constexpr int CPR = BN / 8, RPI = TPB / CPR;  // chunks per row, rows per sweep
+    static_assert(2 * 32 * EROW * 4 <= STAGES * (BM + BN) * DS_ROW * 2, "a staged row pair fits the ring");
+    float *stage = reinterpret_cast<float *>(lds);
+    const int tid = threadIdx.x, c8 = (tid % CPR) * 8, sr0 = tid / CPR, n = n0 + c8;
+    const bool cols = tid < RPI * CPR && n < p.N;
+    // Rope (the rope entry point's guarantees plus rope_d % 8 == 0 and no
+    // residual): a chunk of 8 computed columns lies in one rope head or wholly
+    // past them, and holds two pair-interleaved quads (see rope_store4).
+    const bool rope = ROPE && cols && n < p.rope_cols;
+    const RopeQuad q0 = rope ? rope_quad(n, p.rope_d) : RopeQuad{}, q1 = rope ? rope_quad(n + 4, p.rope_d) : RopeQuad{};
+    // bias by computed column: a rope quad's columns are features lo, hi, lo + 1, hi + 1
+    f32x4 b0 = {}, b1 = {};
+    if (p.bias && rope) {
+        b0 = f32x4{p.bias[q0.lo], p.bias[q0.hi], p.bias[q0.lo + 1], p.bias[q0.hi + 1]};
+        b1 = f32x4{p.bias[q1.lo], p.bias[q1.hi], p.bias[q1.lo + 1], p.bias[q1.hi + 1]};
+    } else if (p.bias && cols) {
+        b0 = *reinterpret_cast<const f32x4 *>(p.bias + n);
+        b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
+    }
     f32x16 acc[TN][TM];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -1190,26 +1211,6 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     // one 16-byte store. The rows are padded by 4 floats so the 32 rows of a
     // block's writes fall in distinct banks. The host guarantees N % 8 == 0,
     // ldc % 8 == 0 and 16-byte aligned C, R and bias.
-    constexpr int EROW = BN + 4;                   // floats per staged row
-    constexpr int CPR = BN / 8, RPI = TPB / CPR;  // chunks per row, rows per sweep
-    static_assert(2 * 32 * EROW * 4 <= STAGES * (BM + BN) * DS_ROW * 2, "a staged row pair fits the ring");
-    float *stage = reinterpret_cast<float *>(lds);
-    const int tid = threadIdx.x, c8 = (tid % CPR) * 8, sr0 = tid / CPR, n = n0 + c8;
-    const bool cols = tid < RPI * CPR && n < p.N;
-    // Rope (the rope entry point's guarantees plus rope_d % 8 == 0 and no
-    // residual): a chunk of 8 computed columns lies in one rope head or wholly
-    // past them, and holds two pair-interleaved quads (see rope_store4).
-    const bool rope = ROPE && cols && n < p.rope_cols;
-    const RopeQuad q0 = rope ? rope_quad(n, p.rope_d) : RopeQuad{}, q1 = rope ? rope_quad(n + 4, p.rope_d) : RopeQuad{};
-    // bias by computed column: a rope quad's columns are features lo, hi, lo + 1, hi + 1
-    f32x4 b0 = {}, b1 = {};
-    if (p.bias && rope) {
-        b0 = f32x4{p.bias[q0.lo], p.bias[q0.hi], p.bias[q0.lo + 1], p.bias[q0.hi + 1]};
-        b1 = f32x4{p.bias[q1.lo], p.bias[q1.hi], p.bias[q1.lo + 1], p.bias[q1.hi + 1]};
-    } else if (p.bias && cols) {
-        b0 = *reinterpret_cast<const f32x4 *>(p.bias + n);
-        b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
-    }
     HX_WAIT_VMCNT(0);
     f16 *C = p.C;
 #pragma unroll
