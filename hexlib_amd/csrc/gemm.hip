@@ -577,10 +577,36 @@ __device__ __forceinline__ void ln_rows_in_lds(f16 (*sA)[BM * DS_ROW], const Gem
 // lgkmcnt(0) with vmcnt and expcnt left at max: this wave's LDS writes are done.
 #define HX_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4))
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+
+// The weight operand of one 32-column block from a [K][N] weight slice held
+// in LDS as it is stored: BN / 64 tiles of [64 k][64 n] (DS_ROW rows, 16-byte
+// chunks XOR-swizzled by k row). The MFMA wants, per lane, 8 consecutive k of
+// column n = ncol + lane % 32: two ds_read_b64_tr_b16, each giving 4 k. Within
+// a 16-lane group lane 4a + b receives element b of the 8 bytes lanes a, a + 4,
+// a + 8, a + 12 address, so lane s addresses k row 4u + s / 4 (of the lane's
+// 8) at columns 4 (s % 4) .. + 3 of its 16-column group.
+__device__ __forceinline__ f16x8 kn_frag(const f16 *bs, int ncol, int q, int lane) {
+    const f16 *tile = bs + (ncol >> 6) * (64 * DS_ROW);
+    const int nn = (ncol & 63) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int k0 = 16 * q + 8 * (lane >> 5) + ((lane & 15) >> 2);
+    v4i16 h[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int row = k0 + 4 * u;
+        h[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16 *) (tile + row * DS_ROW + (((nn >> 3) ^ swz(row)) << 3) + (nn & 7)));
+    }
+    return __builtin_bit_cast(f16x8, (v8i16){h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]});
+}
+
 // WM x WN waves; each owns a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles.
 // LN: A's row block is loaded whole, layer-normalised in LDS, and only B
 // streams through the ring (BM = 64, K <= 64 * LN_KT, 512 <= K).
-template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false, bool LN = false>
+// KN: the weight is [K][N] (matmul_fp16, matmul_epilogue_f16w), copied into
+// the ring as stored (N % 64 == 0) and read through kn_frag.
+template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false, bool LN = false, bool KN = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     constexpr int NW = WM * WN;
     constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
@@ -624,9 +650,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
         }
     }
 
+    static_assert(!KN || (BN % 64 == 0 && !ROPE && !LN), "the [K][N] weight comes in 64-column tiles");
     auto issue = [&](int kt, int st) {
         if constexpr (!LN) lds_copy_slice<BM, NW>(A, p.lda, m0, p.M, kbeg + kt * BK, sA[st]);
-        lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kbeg + kt * BK, sB[st]);
+        if constexpr (KN) {
+            // 64 k rows x 64 columns per tile; a tile wholly past N (N % 64 == 0)
+            // re-reads the last one, in bounds, for columns never stored
+#pragma unroll
+            for (int h = 0; h < BN / 64; ++h)
+                lds_copy_slice<64, NW>(B, p.ldb, kbeg + kt * BK, p.K, min(n0 + 64 * h, p.N - 64), sB[st] + h * (64 * DS_ROW));
+        } else {
+            lds_copy_slice<BN, NW>(B, p.ldb, n0, p.N, kbeg + kt * BK, sB[st]);
+        }
     };
 
     if constexpr (LN) {
@@ -665,7 +700,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
 #pragma unroll
             for (int q = 0; q < BK / 16; ++q) {
                 const int c = 2 * q + (lane >> 5);
-                f.w[q] = *reinterpret_cast<const f16x8 *>(bs + rb * DS_ROW + ((c ^ swz(rb)) << 3));
+                if constexpr (KN) f.w[q] = kn_frag(bs, wn, q, lane);
+                else f.w[q] = *reinterpret_cast<const f16x8 *>(bs + rb * DS_ROW + ((c ^ swz(rb)) << 3));
                 f.x[q] = *reinterpret_cast<const f16x8 *>(as + ra * DS_ROW + ((c ^ swz(ra)) << 3));
             }
         };
@@ -728,7 +764,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
 #pragma unroll
                     for (int j = 0; j < TN; ++j) {
                         const int r = wn + j * 32 + (lane & 31);
-                        wf[q][j] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
+                        if constexpr (KN) wf[q][j] = kn_frag(bs, wn + j * 32, q0 + q, lane);
+                        else wf[q][j] = *reinterpret_cast<const f16x8 *>(bs + r * DS_ROW + ((c ^ swz(r)) << 3));
                     }
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {
@@ -938,8 +975,11 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
 // 2 stages -- 128 KB of LDS). With T = 64 wave w stores block w after the
 // reduction; with T = 32 wave 0 stores.
-template <int T, bool ROPE = false>
+// KN: the weight is [K][N] (N % 64 == 0, T = 64): each sub-slice is its
+// [64 k][64 n] tile as stored, read through kn_frag.
+template <int T, bool ROPE = false, bool KN = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
+    static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
     constexpr int NB = T / 32;                 // 32-row blocks per tile side
     constexpr int STAGES = T == 32 ? 3 : 2;
     constexpr int LOADS = 4 * 2 * (T / 32);     // wave-instructions per stage: 4 sub-slices x (A + B) x T/32
@@ -957,7 +997,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
             lds_copy_slice<T, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
-            lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
+            if constexpr (KN) lds_copy_slice<64, 4>(B, p.ldb, kt * KW_BK + sub * 64, p.K, n0, sB[st][sub]);
+            else lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
     f32x16 acc[NB][NB];   // [column block j][row block i]
@@ -1001,7 +1042,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
             for (int h = 0; h < NB; ++h) {
                 const int rr = h * 32 + r;
-                wf[h] = *reinterpret_cast<const f16x8 *>(bs + rr * DS_ROW + ((c ^ swz(rr)) << 3));
+                if constexpr (KN) wf[h] = kn_frag(bs, h * 32, q, lane);
+                else wf[h] = *reinterpret_cast<const f16x8 *>(bs + rr * DS_ROW + ((c ^ swz(rr)) << 3));
                 xf[h] = *reinterpret_cast<const f16x8 *>(as + rr * DS_ROW + ((c ^ swz(rr)) << 3));
             }
 #pragma unroll
@@ -1691,6 +1733,19 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;
         if (bt.bm && launch_big(p, bt, stages)) return;
     }
+    // the [K][N] weight at few rows: the 64x64 K-across-waves form, where the
+    // W^T rule picks that tile (256 x 768 x 2304: 8.1 us against 9.5 on the
+    // tiled ring); where it picks 32x32 (K = 3072, N = 768) the tiled ring is
+    // faster (12.6 us against 15.3), and so, at 256 x 768 x 768, is this form
+    // (7.6 against 9.1) with no 32-column [K][N] tile
+    const bool kw_kn_ok = MODE == B_KN && batch == 1 && p.K % KW_BK == 0 && p.N % 64 == 0 && p.lda % 8 == 0 &&
+                          p.ldb % 8 == 0 && avec && bvec && (p.M + 63) / 64 <= 65535;
+    const int kw_kn_auto = kw_auto(p.M, p.N);
+    if (kw_kn_ok && (path == 4 || (path == 0 && (kw_kn_auto == 64 || (kw_kn_auto == 32 && p.K <= 768))))) {
+        const dim3 grid((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64));
+        HX_LAUNCH((gemm_nk_kw<64, false, true>), grid, dim3(TPB), 0, p);
+        return;
+    }
     int kw = 0;
     if (kw_ok && path == 4) kw = g_ov_bm.load() == 64 ? 64 : 32;
     else if (kw_ok && path == 0) kw = kw_auto(p.M, p.N);
@@ -1739,10 +1794,25 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     }
     bool lds_direct = MODE == B_NK && p.K % BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                       avec && bvec && p.k_per_split % BK == 0;
+    // the [K][N] weight through the same ring (64-column tiles, transpose
+    // reads), except a one-slice K over more than a round of workgroups,
+    // where the register-staged kernel measured faster (384 x 256x64x256:
+    // 33 us against 48)
+    const long long kn_wgs = (long long) ((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * batch * p.splits;
+    const bool kn_direct = MODE == B_KN && p.K % BK == 0 && p.N % 64 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
+                           avec && bvec && p.k_per_split % BK == 0 && path != 1 && (p.K > BK || kn_wgs <= 512);
     if (path == 1 && !p.rcos) lds_direct = false;   // the rope epilogue exists on this kernel only
     if (p.rcos && !lds_direct) return;                 // unreachable: the rope entry point checks its preconditions
     if (lds_direct && p.rcos && p.splits == 1) {
         launch_lds_rope(p, t);
+    } else if (kn_direct) {
+        if (t.bn < 64) t = {64, 64};   // no 32-column [K][N] form
+        dim3 grid((unsigned) ((p.N + t.bn - 1) / t.bn), (unsigned) ((p.M + t.bm - 1) / t.bm),
+                  (unsigned) (batch * p.splits));
+        if (t.bm == 256) HX_LAUNCH((gemm_nk_lds<256, 128, 3, 2, 2, false, false, true>), grid, dim3(TPB), 0, p);
+        else if (t.bm == 128) HX_LAUNCH((gemm_nk_lds<128, 128, 2, 2, 2, false, false, true>), grid, dim3(TPB), 0, p);
+        else if (t.bm == 32) HX_LAUNCH((gemm_nk_lds<32, 64, 4, 1, 2, false, false, true>), grid, dim3(128), 0, p);
+        else HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, false, false, true>), grid, dim3(TPB), 0, p);
     } else if (lds_direct) {
         dim3 grid((unsigned) ((p.N + t.bn - 1) / t.bn), (unsigned) ((p.M + t.bm - 1) / t.bm),
                   (unsigned) (batch * p.splits));

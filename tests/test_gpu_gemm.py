@@ -602,3 +602,77 @@ def test_big_tile_rope_epilogue(dev, form, M, Kd, heads, d, extra, act):
     want[:, :2 * heads * d] = K.rope_2d_fp16(lin[:, :2 * heads * d].reshape(M, 2 * heads, d), cos, sin).reshape(M, -1)
     np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
     assert K.close_f16(lin, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("tile,splits", [((64, 64), 1), ((128, 128), 1), ((256, 128), 1), ((32, 64), 1),
+                                         ((64, 64), 3), ((128, 128), 2)])
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 2304, 1), (300, 512, 192, 0), (70, 256, 64, 2)])
+def test_kn_weight_direct_path(dev, tile, splits, M, Kd, N, act):
+    """matmul_epilogue_f16w ([K][N] weight, N % 64 == 0) on the direct-to-LDS
+    ring with transpose reads of the weight: bit-identical to the W^T kernel
+    with the same tile and split count (the same per-output MFMA order), and
+    within the harness tolerance of the oracle."""
+    r = rng(24)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dw, dwt, db = dev.up(a), dev.up(w), dev.up(np.ascontiguousarray(w.T)), dev.up(bias)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(tile[0], tile[1], splits, 2) == 1
+    try:
+        dev.lib.matmul_epilogue_f16w_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dwt), dev.ptr(db), dev.ptr(d2), M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    got = dev.down(d1)
+    np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
+    assert K.close_f16(got, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("dims", [(12, 256, 64, 256), (12, 256, 256, 64), (3, 128, 512, 128)])
+def test_batched_matmul_kn_direct_matches_register_path(dev, dims):
+    """The batched matmul_fp16 on the direct-to-LDS [K][N] path equals the
+    register-staged kernel (path 1) within the harness tolerance, and both
+    meet the oracle."""
+    Bn, M, Kd, N = dims
+    r = rng(25)
+    a = h16(r.standard_normal((Bn, M, Kd)))
+    b = h16(r.standard_normal((Bn, Kd, N)) / np.sqrt(Kd))
+    da, dbm = dev.up(a), dev.up(b)
+    outs = []
+    for path in (0, 1):
+        do = dev.empty((Bn, M, N), np.float16)
+        assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, path) == 1
+        try:
+            dev.lib.matmul_fp16(dev.ptr(da), dev.ptr(dbm), dev.ptr(do), Bn, M, Kd, N)
+            dev.check()
+        finally:
+            dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+        outs.append(dev.down(do))
+    want = K.matmul_fp16(a, b)
+    for o in outs:
+        assert K.close_f16(o, want, 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 2304, 1), (256, 768, 768, 0), (200, 512, 192, 2), (256, 3072, 768, 0)])
+def test_kn_weight_kw_path(dev, M, Kd, N, act):
+    """matmul_epilogue_f16w on the 64x64 K-across-waves kernel (path 4 with
+    tile 64x64; K % 256 == 0, N % 64 == 0): bit-identical to the W^T form of
+    the same kernel, and within the harness tolerance of the oracle."""
+    r = rng(26)
+    a = h16(r.standard_normal((M, Kd)))
+    w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dw, dwt, db = dev.up(a), dev.up(w), dev.up(np.ascontiguousarray(w.T)), dev.up(bias)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(64, 64, 0, 4) == 1
+    try:
+        dev.lib.matmul_epilogue_f16w_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dwt), dev.ptr(db), dev.ptr(d2), M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    got = dev.down(d1)
+    np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
+    assert K.close_f16(got, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
