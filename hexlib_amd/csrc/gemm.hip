@@ -36,6 +36,7 @@
 // partial tile to a library workspace and `splitk_reduce` sums the splits in
 // order 0..S-1, adds bias, applies the activation and rounds.
 #include <atomic>
+#include <type_traits>
 #include <mutex>
 #include <vector>
 
@@ -123,10 +124,31 @@ __device__ __forceinline__ void rope_store4(f16 *crow, RopeQuad q, const float v
 // rounded as the reference stores it (the sum is materialised in fp32 first,
 // so the compiler cannot fuse it into the fp16 conversion).
 __device__ __forceinline__ f16 epi(float v, int act, bool has_r, f16 r) {
-    const f16 h = (f16) apply_act(v, act);
+    // the activation's fp32 result is materialised before the fp16 rounding,
+    // so no form fuses the last multiply into the conversion (one rounding
+    // instead of the reference's two)
+    const f16 h = (f16) f32_rounded(apply_act(v, act));
     if (!has_r) return h;
     return (f16) f32_rounded((float) r + (float) h);
 }
+
+// The same with the activation and the residual fixed at compile time: an
+// unrolled epilogue over 16 outputs then holds no branch per output (the
+// runtime form costs about 1.5 us per launch in the batch-1 GEMMs' epilogue).
+template <int ACT>
+__device__ __forceinline__ float act_t(float x) {
+    if constexpr (ACT == 1) return gelu_tanh_f32(x);
+    else if constexpr (ACT == 2) return gelu_erf_f32(x);
+    else return x;
+}
+
+template <int ACT, bool RES>
+__device__ __forceinline__ f16 epi_t(float v, f16 r) {
+    const f16 h = (f16) f32_rounded(act_t<ACT>(v));
+    if constexpr (!RES) return h;
+    else return (f16) f32_rounded((float) r + (float) h);
+}
+
 
 // The unvectorised store of up to 4 consecutive outputs (ragged N, unaligned
 // rows); out of line so the tiled kernels' unrolled epilogues stay small.
@@ -136,6 +158,68 @@ __device__ __noinline__ void store_tail(f16 *dst, int cnt, int act, const f16 *r
 #pragma unroll
     for (int e = 0; e < 4; ++e)
         if (e < cnt) dst[e] = epi(v[e], act, r, r ? r[e] : (f16) 0);
+}
+
+// One 32x32 output block's plain epilogue (the lane holds row m, columns
+// nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order) with the activation and the
+// residual fixed at compile time; kw_store dispatches on the runtime values.
+template <int ACT, bool RES>
+__device__ __forceinline__ void kw_store_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
+                                           bool vec_store) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + (lane >> 5) * 4;
+        float bv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
+        f16 *dst = p.C + (long long) m * p.ldc + n;
+        if (vec_store && n + 3 < p.N) {
+            const f16x4 r4 = RES ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(sum[g * 4 + e] + bv[e], r4[e]);
+            *reinterpret_cast<f16x4 *>(dst) = o;
+        } else {
+            store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr, sum[g * 4] + bv[0],
+                       sum[g * 4 + 1] + bv[1], sum[g * 4 + 2] + bv[2], sum[g * 4 + 3] + bv[3]);
+        }
+    }
+}
+
+// Calls f(integral_constant<int, ACT>, integral_constant<bool, RES>) for the
+// runtime activation (0..2) and residual.
+template <typename F>
+__device__ __forceinline__ void dispatch_epi(int act, bool res, F &&f) {
+    using A0 = std::integral_constant<int, 0>;
+    using A1 = std::integral_constant<int, 1>;
+    using A2 = std::integral_constant<int, 2>;
+    using R0 = std::integral_constant<bool, false>;
+    using R1 = std::integral_constant<bool, true>;
+    if (act == 1) {
+        if (res) f(A1{}, R1{});
+        else f(A1{}, R0{});
+    } else if (act == 2) {
+        if (res) f(A2{}, R1{});
+        else f(A2{}, R0{});
+    } else {
+        if (res) f(A0{}, R1{});
+        else f(A0{}, R0{});
+    }
+}
+
+__device__ __forceinline__ void kw_store(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
+                                         bool vec_store) {
+    const bool res = p.R != nullptr;
+    if (p.act == 1) {
+        if (res) kw_store_t<1, true>(p, m, nb, lane, sum, vec_store);
+        else kw_store_t<1, false>(p, m, nb, lane, sum, vec_store);
+    } else if (p.act == 2) {
+        if (res) kw_store_t<2, true>(p, m, nb, lane, sum, vec_store);
+        else kw_store_t<2, false>(p, m, nb, lane, sum, vec_store);
+    } else {
+        if (res) kw_store_t<0, true>(p, m, nb, lane, sum, vec_store);
+        else kw_store_t<0, false>(p, m, nb, lane, sum, vec_store);
+    }
 }
 
 
@@ -817,6 +901,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
         // of 4 columns is in range as a whole and lies in one head or wholly past
         // the rope heads. The bias and table loads of GB groups are issued before
         // the first of their rotations, so their latencies overlap.
+        dispatch_epi(p.act, false, [&](auto act_c, auto) {
+        constexpr int ACT = decltype(act_c)::value;
         const int half = p.rope_d >> 1;
         // column groups per load batch: 4 for one row block; 1 for more, which keeps
         // the 128x128 tile under 192 VGPRs and so at 2 waves per SIMD
@@ -863,22 +949,26 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
                         if (rope[h]) {
                             float v[4];
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) v[e] = apply_act(acc[j][i][g * 4 + e] + bv[h][e], p.act);
+                            for (int e = 0; e < 4; ++e) v[e] = f32_rounded(act_t<ACT>(acc[j][i][g * 4 + e] + bv[h][e]));
                             rope_store4(crow, q[h], v, c0[h][i], c1[h][i], s0[h][i], s1[h][i]);
                         } else {
                             f16x4 o;
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
-                                o[e] = epi(acc[j][i][g * 4 + e] + bv[h][e], p.act, false, (f16) 0);
+                                o[e] = epi_t<ACT, false>(acc[j][i][g * 4 + e] + bv[h][e], (f16) 0);
                             *reinterpret_cast<f16x4 *>(crow + n) = o;
                         }
                     }
                 }
             }
         }
+        });
         return;
     }
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
+    dispatch_epi(p.act, p.R != nullptr, [&](auto act_c, auto res_c) {
+    constexpr int ACT = decltype(act_c)::value;
+    constexpr bool RES = decltype(res_c)::value;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -894,10 +984,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
                 if (m >= p.M) continue;
                 f16 *dst = C + (long long) m * p.ldc + n;
                 if (vec_store && n + 3 < p.N) {
-                    const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
+                    const f16x4 r4 = RES ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
                     f16x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R, r4[e]);
+                    for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(acc[j][i][g * 4 + e] + bv[e], r4[e]);
                     *reinterpret_cast<f16x4 *>(dst) = o;
                 } else {
                     store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr,
@@ -907,6 +997,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
             }
         }
     }
+    });
 }
 
 // ---- W^T small-M path: K split across the waves, 256-deep stages --------------
@@ -928,7 +1019,8 @@ constexpr int KW_BK = 256;
 // One 32x32 output block's rope epilogue (the lane holds row m, columns
 // nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order): the same arithmetic as
 // gemm_nk_lds's rope epilogue, with every bias and table load issued first.
-__device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
+template <int ACT>
+__device__ __forceinline__ void store_block_rope_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
     const int half = p.rope_d >> 1;
     const int mc = min(m, p.M - 1);
     RopeQuad q[4];
@@ -961,15 +1053,21 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
         if (rope[g]) {
             float x[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = apply_act(v[g * 4 + e] + bv[g][e], p.act);
+            for (int e = 0; e < 4; ++e) x[e] = f32_rounded(act_t<ACT>(v[g * 4 + e] + bv[g][e]));
             rope_store4(crow, q[g], x, c0[g], c1[g], s0[g], s1[g]);
         } else {
             f16x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = epi(v[g * 4 + e] + bv[g][e], p.act, false, (f16) 0);
+            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, false>(v[g * 4 + e] + bv[g][e], (f16) 0);
             *reinterpret_cast<f16x4 *>(crow + n) = o;
         }
     }
+}
+
+__device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
+    if (p.act == 1) store_block_rope_t<1>(p, m, nb, lane, v);
+    else if (p.act == 2) store_block_rope_t<2>(p, m, nb, lane, v);
+    else store_block_rope_t<0>(p, m, nb, lane, v);
 }
 
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
@@ -1086,24 +1184,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     if (m >= p.M) return;
     f16 *C = p.C;
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int n = n0 + (blk % NB) * 32 + g * 8 + (lane >> 5) * 4;
-        float bv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
-        f16 *dst = C + (long long) m * p.ldc + n;
-        if (vec_store && n + 3 < p.N) {
-            const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
-            f16x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = epi(sum[g * 4 + e] + bv[e], p.act, p.R, r4[e]);
-            *reinterpret_cast<f16x4 *>(dst) = o;
-        } else {
-            store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr, sum[g * 4] + bv[0],
-                       sum[g * 4 + 1] + bv[1], sum[g * 4 + 2] + bv[2], sum[g * 4 + 3] + bv[3]);
-        }
-    }
+    kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store);
 }
 
 // ---- W^T large-M path: big wave tiles, fragment reads under the MFMAs ----------
