@@ -521,6 +521,9 @@ struct Gemm {
         f16 *C = p.C + (long long) bz * p.sC;
         const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) &&
                                (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
+        dispatch_epi(p.act, p.R != nullptr, [&](auto act_c, auto res_c) {
+        constexpr int ACT = decltype(act_c)::value;
+        constexpr bool RES = decltype(res_c)::value;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -535,10 +538,10 @@ struct Gemm {
                     if (m >= p.M) continue;
                     f16 *dst = C + (long long) m * p.ldc + n;
                     if (vec_store && n + 3 < p.N) {
-                        const f16x4 r4 = p.R ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
+                        const f16x4 r4 = RES ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
                         f16x4 o;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) o[e] = epi(acc[j][i][g * 4 + e] + bv[e], p.act, p.R, r4[e]);
+                        for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(acc[j][i][g * 4 + e] + bv[e], r4[e]);
                         *reinterpret_cast<f16x4 *>(dst) = o;
                     } else {
                         store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr,
@@ -548,6 +551,7 @@ struct Gemm {
                 }
             }
         }
+        });
     }
 };
 
@@ -1386,8 +1390,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
                     float x0[4], x1[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        x0[e] = apply_act(v0[e] + b0[e], p.act);
-                        x1[e] = apply_act(v1[e] + b1[e], p.act);
+                        x0[e] = f32_rounded(apply_act(v0[e] + b0[e], p.act));
+                        x1[e] = f32_rounded(apply_act(v1[e] + b1[e], p.act));
                     }
                     f16 *crow = C + (long long) m * p.ldc;
                     rope_store4(crow, q0, x0, float2{t.c[0], t.c[1]}, float2{t.c[4], t.c[5]},
@@ -1403,22 +1407,26 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
             return p.R && sr < 64 && m < p.M ? *reinterpret_cast<const f16x8 *>(p.R + (long long) m * p.ldr + n)
                                              : f16x8{};
         };
-        f16x8 rn = resid(sr0);
-        for (int sr = sr0; sr < 64; sr += RPI) {
-            const f16x8 r8 = rn;
-            rn = resid(sr + RPI);
-            const int m = row_of(sr);
-            if (m >= p.M) continue;
-            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
-            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
-            f16x8 o;
+        dispatch_epi(p.act, p.R != nullptr, [&](auto act_c, auto res_c) {
+            constexpr int ACT = decltype(act_c)::value;
+            constexpr bool RES = decltype(res_c)::value;
+            f16x8 rn = RES ? resid(sr0) : f16x8{};
+            for (int sr = sr0; sr < 64; sr += RPI) {
+                const f16x8 r8 = rn;
+                if constexpr (RES) rn = resid(sr + RPI);
+                const int m = row_of(sr);
+                if (m >= p.M) continue;
+                const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
+                const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
+                f16x8 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                o[e] = epi(v0[e] + b0[e], p.act, p.R, r8[e]);
-                o[e + 4] = epi(v1[e] + b1[e], p.act, p.R, r8[e + 4]);
+                for (int e = 0; e < 4; ++e) {
+                    o[e] = epi_t<ACT, RES>(v0[e] + b0[e], r8[e]);
+                    o[e + 4] = epi_t<ACT, RES>(v1[e] + b1[e], r8[e + 4]);
+                }
+                *reinterpret_cast<f16x8 *>(C + (long long) m * p.ldc + n) = o;
             }
-            *reinterpret_cast<f16x8 *>(C + (long long) m * p.ldc + n) = o;
-        }
+        });
     }
 }
 
@@ -1603,7 +1611,7 @@ __global__ __launch_bounds__(TPB) void splitk_reduce_rope(const float *__restric
             const int f[4] = {r.lo, r.hi, r.lo + 1, r.hi + 1};
             float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = apply_act(s[e] + (bias ? bias[f[e]] : 0.0f), act);
+            for (int e = 0; e < 4; ++e) o[e] = f32_rounded(apply_act(s[e] + (bias ? bias[f[e]] : 0.0f), act));
             const long long ld = M, t = (long long) r.t * ld + m, th = t + (rope_d >> 1) * ld;
             rope_store4(crow, r, o, float2{rcos[t], rcos[t + ld]}, float2{rcos[th], rcos[th + ld]},
                         float2{rsin[t], rsin[t + ld]}, float2{rsin[th], rsin[th + ld]});
