@@ -163,15 +163,37 @@ __device__ __noinline__ void store_tail(f16 *dst, int cnt, int act, const f16 *r
 // One 32x32 output block's plain epilogue (the lane holds row m, columns
 // nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order) with the activation and the
 // residual fixed at compile time; kw_store dispatches on the runtime values.
+// The bias of one 32-column block, columns nb .. nb + 31 (nb wave-uniform), read
+// through the constant address space: uniform addresses become scalar loads,
+// issued at kernel start and tracked apart from the vector loads of the ring.
+struct BlockBias {
+    float v[32];
+};
+
+__device__ __forceinline__ BlockBias load_block_bias(const GemmArgs &p, int nb) {
+    typedef const __attribute__((address_space(4))) float cfloat;
+    BlockBias b;
+    const int nbu = __builtin_amdgcn_readfirstlane(nb);
+    if (p.bias && nbu + 32 <= p.N) {
+        const cfloat *src = reinterpret_cast<const cfloat *>(reinterpret_cast<uintptr_t>(p.bias + nbu));
+#pragma unroll
+        for (int k = 0; k < 32; ++k) b.v[k] = src[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) b.v[k] = (p.bias && nbu + k < p.N) ? p.bias[nbu + k] : 0.0f;
+    }
+    return b;
+}
+
 template <int ACT, bool RES>
 __device__ __forceinline__ void kw_store_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
-                                           bool vec_store) {
+                                           bool vec_store, const BlockBias &bb) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
         float bv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.0f;
+        for (int e = 0; e < 4; ++e) bv[e] = (lane >> 5) ? bb.v[g * 8 + 4 + e] : bb.v[g * 8 + e];
         f16 *dst = p.C + (long long) m * p.ldc + n;
         if (vec_store && n + 3 < p.N) {
             const f16x4 r4 = RES ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
@@ -208,17 +230,17 @@ __device__ __forceinline__ void dispatch_epi(int act, bool res, F &&f) {
 }
 
 __device__ __forceinline__ void kw_store(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
-                                         bool vec_store) {
+                                         bool vec_store, const BlockBias &bb) {
     const bool res = p.R != nullptr;
     if (p.act == 1) {
-        if (res) kw_store_t<1, true>(p, m, nb, lane, sum, vec_store);
-        else kw_store_t<1, false>(p, m, nb, lane, sum, vec_store);
+        if (res) kw_store_t<1, true>(p, m, nb, lane, sum, vec_store, bb);
+        else kw_store_t<1, false>(p, m, nb, lane, sum, vec_store, bb);
     } else if (p.act == 2) {
-        if (res) kw_store_t<2, true>(p, m, nb, lane, sum, vec_store);
-        else kw_store_t<2, false>(p, m, nb, lane, sum, vec_store);
+        if (res) kw_store_t<2, true>(p, m, nb, lane, sum, vec_store, bb);
+        else kw_store_t<2, false>(p, m, nb, lane, sum, vec_store, bb);
     } else {
-        if (res) kw_store_t<0, true>(p, m, nb, lane, sum, vec_store);
-        else kw_store_t<0, false>(p, m, nb, lane, sum, vec_store);
+        if (res) kw_store_t<0, true>(p, m, nb, lane, sum, vec_store, bb);
+        else kw_store_t<0, false>(p, m, nb, lane, sum, vec_store, bb);
     }
 }
 
@@ -1103,6 +1125,9 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             else lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
+    // the plain epilogue's bias for this wave's output block, by scalar loads now
+    BlockBias bbias{};
+    if constexpr (!ROPE) bbias = load_block_bias(p, n0 + (wave % NB) * 32);
     f32x16 acc[NB][NB];   // [column block j][row block i]
 #pragma unroll
     for (int j = 0; j < NB; ++j)
@@ -1188,7 +1213,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     if (m >= p.M) return;
     f16 *C = p.C;
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
-    kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store);
+    kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store, bbias);
 }
 
 // ---- W^T large-M path: big wave tiles, fragment reads under the MFMAs ----------
