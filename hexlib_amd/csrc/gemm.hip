@@ -185,9 +185,27 @@ __device__ __forceinline__ BlockBias load_block_bias(const GemmArgs &p, int nb) 
     return b;
 }
 
+// The residual of one 32x32 block (the lane's 4 groups of 4 columns), loaded
+// at kernel start, before the ring's first copies, so its latency is spent
+// under the K loop; zero where the vector store does not apply.
+struct BlockRes {
+    f16x4 r[4];
+};
+
+__device__ __forceinline__ BlockRes load_block_res(const GemmArgs &p, int m, int nb, int lane, bool vec_store) {
+    BlockRes t;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + (lane >> 5) * 4;
+        t.r[g] = p.R && vec_store && m < p.M && n + 3 < p.N
+                     ? *reinterpret_cast<const f16x4 *>(p.R + (long long) m * p.ldr + n) : f16x4{};
+    }
+    return t;
+}
+
 template <int ACT, bool RES>
 __device__ __forceinline__ void kw_store_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
-                                           bool vec_store, const BlockBias &bb) {
+                                           bool vec_store, const BlockBias &bb, const BlockRes &br) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
@@ -196,10 +214,9 @@ __device__ __forceinline__ void kw_store_t(const GemmArgs &p, int m, int nb, int
         for (int e = 0; e < 4; ++e) bv[e] = (lane >> 5) ? bb.v[g * 8 + 4 + e] : bb.v[g * 8 + e];
         f16 *dst = p.C + (long long) m * p.ldc + n;
         if (vec_store && n + 3 < p.N) {
-            const f16x4 r4 = RES ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
             f16x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(sum[g * 4 + e] + bv[e], r4[e]);
+            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(sum[g * 4 + e] + bv[e], br.r[g][e]);
             *reinterpret_cast<f16x4 *>(dst) = o;
         } else {
             store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr, sum[g * 4] + bv[0],
@@ -230,17 +247,17 @@ __device__ __forceinline__ void dispatch_epi(int act, bool res, F &&f) {
 }
 
 __device__ __forceinline__ void kw_store(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
-                                         bool vec_store, const BlockBias &bb) {
+                                         bool vec_store, const BlockBias &bb, const BlockRes &br) {
     const bool res = p.R != nullptr;
     if (p.act == 1) {
-        if (res) kw_store_t<1, true>(p, m, nb, lane, sum, vec_store, bb);
-        else kw_store_t<1, false>(p, m, nb, lane, sum, vec_store, bb);
+        if (res) kw_store_t<1, true>(p, m, nb, lane, sum, vec_store, bb, br);
+        else kw_store_t<1, false>(p, m, nb, lane, sum, vec_store, bb, br);
     } else if (p.act == 2) {
-        if (res) kw_store_t<2, true>(p, m, nb, lane, sum, vec_store, bb);
-        else kw_store_t<2, false>(p, m, nb, lane, sum, vec_store, bb);
+        if (res) kw_store_t<2, true>(p, m, nb, lane, sum, vec_store, bb, br);
+        else kw_store_t<2, false>(p, m, nb, lane, sum, vec_store, bb, br);
     } else {
-        if (res) kw_store_t<0, true>(p, m, nb, lane, sum, vec_store, bb);
-        else kw_store_t<0, false>(p, m, nb, lane, sum, vec_store, bb);
+        if (res) kw_store_t<0, true>(p, m, nb, lane, sum, vec_store, bb, br);
+        else kw_store_t<0, false>(p, m, nb, lane, sum, vec_store, bb, br);
     }
 }
 
@@ -1125,9 +1142,17 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             else lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
-    // the plain epilogue's bias for this wave's output block, by scalar loads now
+    // the plain epilogue's bias (scalar loads) and residual for this wave's
+    // output block, issued now, ahead of the ring's first copies
     BlockBias bbias{};
-    if constexpr (!ROPE) bbias = load_block_bias(p, n0 + (wave % NB) * 32);
+    BlockRes bres{};
+    if constexpr (!ROPE) {
+        bbias = load_block_bias(p, n0 + (wave % NB) * 32);
+        if (p.R && wave < NB * NB) {
+            const bool vs = (p.ldc & 3) == 0 && hx_aligned8(p.C) && (p.ldr & 3) == 0 && hx_aligned8(p.R);
+            bres = load_block_res(p, m0 + (wave / NB) * 32 + (lane & 31), n0 + (wave % NB) * 32, lane, vs);
+        }
+    }
     f32x16 acc[NB][NB];   // [column block j][row block i]
 #pragma unroll
     for (int j = 0; j < NB; ++j)
@@ -1213,7 +1238,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     if (m >= p.M) return;
     f16 *C = p.C;
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
-    kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store, bbias);
+    kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store, bbias, bres);
 }
 
 // ---- W^T large-M path: big wave tiles, fragment reads under the MFMAs ----------
