@@ -29,9 +29,11 @@
 //                 are in-lane plus one exchange with lane l ^ 32.
 //   O^T = V^T P^T A = V^T rows (d), B = P^T: the B operand is the lane's own
 //                 16 probabilities, provided A's k index means the same key.
-// To make that true the K rows are loaded in a permuted key order: S^T row r
-// holds key kperm(r), chosen so that P's k index 8h + j of chunk c is key
-// 16c + 8h + j; the V^T operand then needs 8 consecutive keys of one d. The V
+// To make that true S^T row r holds key kperm(r), chosen so that P's k index
+// 8h + j of chunk c is key 16c + 8h + j: the K tile goes to a wave-private
+// LDS tile as loaded (8 lanes per key row, so a load touches 8 rows, not the
+// 32 of the operand layout) and the operand reads row kperm(r) of it. The
+// V^T operand then needs 8 consecutive keys of one d. The V
 // tile goes to a wave-private LDS tile as loaded ([key][d], 16-byte writes,
 // 192-byte rows) and each V^T operand is two ds_read_b64_tr_b16: within each
 // 16-lane group, lane 4a + b receives element b of the 8 bytes that lanes a,
@@ -65,19 +67,23 @@ __device__ __forceinline__ int kperm(int r) {
 
 template <int D>
 struct KvTile {
-    f16x8 k[D / 16];       // this lane's K row chunks (A operand of S^T)
+    f16x8 k[D / 16];       // this lane's 16-byte pieces of the K tile
     f16x8 v[D / 16];       // this lane's 16-byte pieces of the V tile
 };
 
 template <int D>
 __device__ __forceinline__ void load_tile(const f16 *__restrict__ kb, long long ldk, const f16 *__restrict__ vb,
-                                          long long ldv, int T, int kt, int krow_key, int lane, KvTile<D> &t) {
+                                          long long ldv, int T, int kt, int lane, KvTile<D> &t) {
     constexpr int VCH = D / 8;
-    const int hl = lane >> 5;
-    const int key = min(kt + krow_key, T - 1);   // rows past T are masked after the product
+    // K as V: 8 lanes per 128-byte key row, so one load touches 8 rows (the
+    // MFMA operand layout would touch 32); rows past T repeat row T - 1 and
+    // are masked after the product
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-        t.k[kk] = *reinterpret_cast<const f16x8 *>(kb + key * ldk + 16 * kk + 8 * hl);
+    for (int i = 0; i < D / 16; ++i) {
+        const int e = lane + 64 * i;
+        const int key = min(kt + e / VCH, T - 1);
+        t.k[i] = *reinterpret_cast<const f16x8 *>(kb + key * ldk + (e % VCH) * 8);
+    }
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) {
         const int e = lane + 64 * i;
@@ -99,6 +105,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     constexpr int VCH = D / 8;   // 16-byte chunks per V row
     constexpr int V_STRIDE = v_stride<D>();
     __shared__ __attribute__((aligned(16))) f16 v_all[WAVES][KT * V_STRIDE];
+    // the K tile, wave-private, as loaded: 144-byte rows keep the 16 rows one
+    // ds_read_b128 phase reads in distinct banks
+    constexpr int K_STRIDE = D + 8;
+    __shared__ __attribute__((aligned(16))) f16 k_all[WAVES][KT * K_STRIDE];
     __shared__ float part_o[WAVES][QT][D + 1];
     __shared__ float part_m[WAVES][QT], part_l[WAVES][QT];
 
@@ -112,6 +122,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
     const int q0 = blockIdx.x * QT;
     f16 *vt = v_all[wave];
+    f16 *ktl = k_all[wave];
     // transpose-read addresses (halves) within the tile: key 8 hl + 4 u + s / 4,
     // d 16 ((lane / 16) % 2) + 4 (s % 4), s = lane % 16; chunk c adds 16 keys, d tile t 32 d
     const int tr_off = (8 * hl + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
@@ -133,10 +144,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
 
     KvTile<D> cur, nxt;
     int kt = wave * KT;
-    if (kt < T) load_tile<D>(kb, ldqk, vb, ldv, T, kt, krow_key, lane, cur);
+    if (kt < T) load_tile<D>(kb, ldqk, vb, ldv, T, kt, lane, cur);
     for (; kt < T; kt += WAVES * KT) {
         const int kn = kt + WAVES * KT;
-        if (kn < T) load_tile<D>(kb, ldqk, vb, ldv, T, kn, krow_key, lane, nxt);
+        if (kn < T) load_tile<D>(kb, ldqk, vb, ldv, T, kn, lane, nxt);
 
         // V tile -> wave-private LDS as loaded, [key][d]
 #pragma unroll
@@ -145,9 +156,20 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
             *reinterpret_cast<f16x8 *>(vt + (e / VCH) * V_STRIDE + (e % VCH) * 8) = cur.v[i];
         }
 
+        // K tile -> wave-private LDS as loaded; the S^T operand is key row
+        // kperm(c32) of it
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) {
+            const int e = lane + 64 * i;
+            *reinterpret_cast<f16x8 *>(ktl + (e / VCH) * K_STRIDE + (e % VCH) * 8) = cur.k[i];
+        }
+        f16x8 kf[KC];
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk)
+            kf[kk] = *reinterpret_cast<const f16x8 *>(ktl + krow_key * K_STRIDE + 16 * kk + 8 * hl);
         f32x16 s = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < KC; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.k[kk], qf[kk], s, 0, 0, 0);
+        for (int kk = 0; kk < KC; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], s, 0, 0, 0);
 
         // element i of this lane is key kt + 16 (i / 8) + 8 hl + i % 8
         float tmax = -INFINITY;
