@@ -1062,9 +1062,10 @@ constexpr int KW_BK = 256;
 // One 32x32 output block's rope epilogue (the lane holds row m, columns
 // nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order): the same arithmetic as
 // gemm_nk_lds's rope epilogue, with every bias and table load issued first.
-template <int ACT>
+template <int ACT, int RD>
 __device__ __forceinline__ void store_block_rope_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
-    const int half = p.rope_d >> 1;
+    const int rope_d = RD ? RD : p.rope_d;   // RD: the head width fixed at compile time (0: runtime)
+    const int half = rope_d >> 1;
     const int mc = min(m, p.M - 1);
     RopeQuad q[4];
     bool rope[4];
@@ -1074,7 +1075,7 @@ __device__ __forceinline__ void store_block_rope_t(const GemmArgs &p, int m, int
     for (int g = 0; g < 4; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
         rope[g] = n < p.rope_cols;
-        q[g] = rope[g] ? rope_quad(n, p.rope_d) : RopeQuad{n, n + 1, 0};
+        q[g] = rope[g] ? rope_quad(n, rope_d) : RopeQuad{n, n + 1, 0};
         const int f[4] = {q[g].lo, rope[g] ? q[g].hi : n + 1, q[g].lo + (rope[g] ? 1 : 2),
                           rope[g] ? q[g].hi + 1 : n + 3};
 #pragma unroll
@@ -1107,10 +1108,18 @@ __device__ __forceinline__ void store_block_rope_t(const GemmArgs &p, int m, int
     }
 }
 
+// The encoder's head width (64) gets its own form: the column-to-pair mapping
+// then takes shifts and masks instead of integer divisions.
 __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
-    if (p.act == 1) store_block_rope_t<1>(p, m, nb, lane, v);
-    else if (p.act == 2) store_block_rope_t<2>(p, m, nb, lane, v);
-    else store_block_rope_t<0>(p, m, nb, lane, v);
+    if (p.rope_d == 64) {
+        if (p.act == 1) store_block_rope_t<1, 64>(p, m, nb, lane, v);
+        else if (p.act == 2) store_block_rope_t<2, 64>(p, m, nb, lane, v);
+        else store_block_rope_t<0, 64>(p, m, nb, lane, v);
+    } else {
+        if (p.act == 1) store_block_rope_t<1, 0>(p, m, nb, lane, v);
+        else if (p.act == 2) store_block_rope_t<2, 0>(p, m, nb, lane, v);
+        else store_block_rope_t<0, 0>(p, m, nb, lane, v);
+    }
 }
 
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
