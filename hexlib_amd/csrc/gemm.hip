@@ -1127,9 +1127,14 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
 // reduction; with T = 32 wave 0 stores.
 // KN: the weight is [K][N] (N % 64 == 0, T = 64): each sub-slice is its
 // [64 k][64 n] tile as stored, read through kn_frag.
-template <int T, bool ROPE = false, bool KN = false>
+// Q8: the weight is q8_0 W^T ([N][K/32] blocks of an fp16 scale and 32 int8,
+// 34 bytes, 2-byte aligned): each stage's blocks are loaded into registers
+// while the previous stage is multiplied, then dequantized to fp16(d * q)
+// into the same LDS layout the fp16 copies fill.
+template <int T, bool ROPE = false, bool KN = false, bool Q8 = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
+    static_assert(!Q8 || (!KN && !ROPE), "q8_0 weights come as W^T blocks");
     constexpr int NB = T / 32;                 // 32-row blocks per tile side
     constexpr int STAGES = T == 32 ? 3 : 2;
     constexpr int LOADS = 4 * 2 * (T / 32);     // wave-instructions per stage: 4 sub-slices x (A + B) x T/32
@@ -1147,8 +1152,40 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
             lds_copy_slice<T, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
-            if constexpr (KN) lds_copy_slice<64, 4>(B, p.ldb, kt * KW_BK + sub * 64, p.K, n0, sB[st][sub]);
+            if constexpr (Q8) continue;
+            else if constexpr (KN) lds_copy_slice<64, 4>(B, p.ldb, kt * KW_BK + sub * 64, p.K, n0, sB[st][sub]);
             else lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
+        }
+    };
+    // q8_0: a stage is T rows x 8 blocks; thread t takes blocks t + 256 u
+    constexpr int NQ = Q8 ? T * 8 / TPB : 1;
+    struct Q8Regs {
+        float d[NQ];
+        uint32_t qs[NQ][8];
+    };
+    auto q8_load = [&](int kt, Q8Regs &q) {
+        const uint8_t *Bq = reinterpret_cast<const uint8_t *>(p.B);
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
+            const uint8_t *src = Bq + (long long) min(n0 + row, p.N - 1) * p.ldb + (kt * 8 + kb) * 34;
+            load_q8_half(src, 0, q.d[u], q.qs[u]);
+            float d1;
+            load_q8_half(src, 1, d1, q.qs[u] + 4);
+        }
+    };
+    auto q8_store = [&](int st, const Q8Regs &q) {
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
+            f16 *dst = sB[st][kb >> 1] + row * DS_ROW;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                f16x8 v;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = q8_val(q.d[u], q.qs[u] + 4 * (c >> 1), (c & 1) * 8 + j);
+                *reinterpret_cast<f16x8 *>(dst + ((((kb & 1) * 4 + c) ^ swz(row)) << 3)) = v;
+            }
         }
     };
     // the plain epilogue's bias (scalar loads) and residual for this wave's
@@ -1179,22 +1216,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     for (int s = 0; s < (FULL ? STAGES : STAGES - 1); ++s)
         if (s < KT) issue(s, s);
     const int r = lane & 31;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int st = kt % STAGES;
-        // stage kt's copies are done (this wave) once at most the later ones remain
-        if constexpr (FULL) {
-            if (kt == 0 && KT >= 2) HX_WAIT_VMCNT(LOADS);
-            else HX_WAIT_VMCNT(0);
-        } else {
-            if (kt + STAGES - 1 <= KT) HX_WAIT_VMCNT(LOADS * (STAGES - 2));
-            else HX_WAIT_VMCNT(0);
-        }
-        __builtin_amdgcn_s_barrier();   // and every wave's; stage kt - 1's reads are done
-        if constexpr (FULL) {
-            if (kt > 0 && kt + 1 < KT) issue(kt + 1, (kt + 1) % 2);
-        } else {
-            if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        }
+    auto mma_stage = [&](int st) {
         const f16 *as = sA[st][wave], *bs = sB[st][wave];
 #pragma unroll
         for (int q = 0; q < BK / 16; ++q) {
@@ -1212,6 +1234,49 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
                 for (int i = 0; i < NB; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[j][i], 0, 0, 0);
         }
+    };
+    if constexpr (Q8) {
+        // the prologue above sent stage 0's A (and with 2 slots stage 1's); here
+        // stage 0's weight is loaded and dequantized. Each iteration waits for
+        // everything (stage kt's A copies, every wave's stage-kt dequantized
+        // writes), sends stage kt + 1's A to its slot and loads its q8_0 blocks,
+        // multiplies stage kt, then dequantizes stage kt + 1 into its slot --
+        // free, since every wave has passed this iteration's barrier after
+        // multiplying stage kt + 1 - STAGES.
+        Q8Regs q8r;
+        q8_load(0, q8r);
+        q8_store(0, q8r);
+        for (int kt = 0; kt < KT; ++kt) {
+            const int st = kt % STAGES;
+            HX_WAIT_VMCNT(0);
+            HX_WAIT_LGKM0();
+            __builtin_amdgcn_s_barrier();
+            if (kt + 1 < KT) {
+                if (kt + 1 >= (FULL ? STAGES : STAGES - 1)) issue(kt + 1, (kt + 1) % STAGES);   // else the prologue sent it
+                q8_load(kt + 1, q8r);
+            }
+            mma_stage(st);
+            if (kt + 1 < KT) q8_store((kt + 1) % STAGES, q8r);
+        }
+    } else {
+    for (int kt = 0; kt < KT; ++kt) {
+        const int st = kt % STAGES;
+        // stage kt's copies are done (this wave) once at most the later ones remain
+        if constexpr (FULL) {
+            if (kt == 0 && KT >= 2) HX_WAIT_VMCNT(LOADS);
+            else HX_WAIT_VMCNT(0);
+        } else {
+            if (kt + STAGES - 1 <= KT) HX_WAIT_VMCNT(LOADS * (STAGES - 2));
+            else HX_WAIT_VMCNT(0);
+        }
+        __builtin_amdgcn_s_barrier();   // and every wave's; stage kt - 1's reads are done
+        if constexpr (FULL) {
+            if (kt > 0 && kt + 1 < KT) issue(kt + 1, (kt + 1) % 2);
+        } else {
+            if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        }
+        mma_stage(st);
+    }
     }
     // combine the waves' partial tiles: [wave][block][e/4][lane][4] floats over the ring
     HX_WAIT_VMCNT(0);
@@ -1893,6 +1958,23 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         const dim3 grid((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64));
         HX_LAUNCH((gemm_nk_kw<64, false, true>), grid, dim3(TPB), 0, p);
         return;
+    }
+    // q8_0 weights at few rows: the K-across-waves kernel with the weight
+    // dequantized into LDS (path 1 keeps the register-staged kernel)
+    const bool kw_q8_ok = MODE == B_Q8K && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && avec &&
+                          (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w && path != 1;
+    if (kw_q8_ok) {
+        const int kq = path == 4 ? (g_ov_bm.load() == 64 ? 64 : 32) : (path == 0 ? kw_auto(p.M, p.N) : 0);
+        if (kq == 64) {
+            HX_LAUNCH((gemm_nk_kw<64, false, false, true>), dim3((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64)),
+                      dim3(TPB), 0, p);
+            return;
+        }
+        if (kq == 32) {
+            HX_LAUNCH((gemm_nk_kw<32, false, false, true>), dim3((unsigned) ((p.N + 31) / 32), (unsigned) ((p.M + 31) / 32)),
+                      dim3(TPB), 0, p);
+            return;
+        }
     }
     int kw = 0;
     if (kw_ok && path == 4) kw = g_ov_bm.load() == 64 ? 64 : 32;
