@@ -1127,14 +1127,18 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
 // reduction; with T = 32 wave 0 stores.
 // KN: the weight is [K][N] (N % 64 == 0, T = 64): each sub-slice is its
 // [64 k][64 n] tile as stored, read through kn_frag.
-// Q8: the weight is q8_0 W^T ([N][K/32] blocks of an fp16 scale and 32 int8,
-// 34 bytes, 2-byte aligned): each stage's blocks are loaded into registers
-// while the previous stage is multiplied, then dequantized to fp16(d * q)
-// into the same LDS layout the fp16 copies fill.
-template <int T, bool ROPE = false, bool KN = false, bool Q8 = false>
+// QB: the weight is block-quantized W^T, [N][K/32] blocks of an fp16 scale
+// and 32 codes, 2-byte aligned -- QB = 8: q8_0 (32 int8, 34 bytes), QB = 4:
+// q4_0 grouped along K (16 bytes of nibbles, 18 bytes). Each stage's blocks are
+// loaded into registers while the previous stage is multiplied, then
+// dequantized (fp16(d * q), fp16(d * (q - 8))) into the same LDS layout the
+// fp16 copies fill.
+template <int T, bool ROPE = false, bool KN = false, int QB = 0>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
-    static_assert(!Q8 || (!KN && !ROPE), "q8_0 weights come as W^T blocks");
+    static_assert(QB == 0 || (!KN && !ROPE && (QB == 8 || QB == 4)), "quantized weights come as W^T blocks");
+    constexpr bool Q8 = QB != 0;                 // a block-quantized weight (either format)
+    constexpr int QBYTES = QB == 8 ? 34 : 18;
     constexpr int NB = T / 32;                 // 32-row blocks per tile side
     constexpr int STAGES = T == 32 ? 3 : 2;
     constexpr int LOADS = 4 * 2 * (T / 32);     // wave-instructions per stage: 4 sub-slices x (A + B) x T/32
@@ -1168,10 +1172,14 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
-            const uint8_t *src = Bq + (long long) min(n0 + row, p.N - 1) * p.ldb + (kt * 8 + kb) * 34;
-            load_q8_half(src, 0, q.d[u], q.qs[u]);
-            float d1;
-            load_q8_half(src, 1, d1, q.qs[u] + 4);
+            const uint8_t *src = Bq + (long long) min(n0 + row, p.N - 1) * p.ldb + (kt * 8 + kb) * QBYTES;
+            if constexpr (QB == 8) {
+                load_q8_half(src, 0, q.d[u], q.qs[u]);
+                float d1;
+                load_q8_half(src, 1, d1, q.qs[u] + 4);
+            } else {
+                load_q4_block(src, q.d[u], q.qs[u]);
+            }
         }
     };
     auto q8_store = [&](int st, const Q8Regs &q) {
@@ -1183,7 +1191,10 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             for (int c = 0; c < 4; ++c) {
                 f16x8 v;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = q8_val(q.d[u], q.qs[u] + 4 * (c >> 1), (c & 1) * 8 + j);
+                for (int j = 0; j < 8; ++j) {
+                    if constexpr (QB == 8) v[j] = q8_val(q.d[u], q.qs[u] + 4 * (c >> 1), (c & 1) * 8 + j);
+                    else v[j] = q4_val(q.d[u], nib(q.qs[u], (c * 8 + j) & 15, ((c * 8 + j) >> 4) * 4));
+                }
                 *reinterpret_cast<f16x8 *>(dst + ((((kb & 1) * 4 + c) ^ swz(row)) << 3)) = v;
             }
         }
@@ -1959,19 +1970,23 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         HX_LAUNCH((gemm_nk_kw<64, false, true>), grid, dim3(TPB), 0, p);
         return;
     }
-    // q8_0 weights at few rows: the K-across-waves kernel with the weight
-    // dequantized into LDS (path 1 keeps the register-staged kernel)
-    const bool kw_q8_ok = MODE == B_Q8K && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && avec &&
-                          (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w && path != 1;
-    if (kw_q8_ok) {
-        const int kq = path == 4 ? (g_ov_bm.load() == 64 ? 64 : 32) : (path == 0 ? kw_auto(p.M, p.N) : 0);
+    // q8_0 and K-grouped q4_0 weights at few rows: the K-across-waves kernel
+    // with the weight dequantized into LDS (path 1 keeps the register-staged
+    // kernel). Up to K = 3072 (a sweep on MI355X: 256 x 768 x 2304 q8_0 8.2 us
+    // against 12.0, cfg 5's 2048 x 2048 q4_0 at M = 1 10.0 against 12.1); at
+    // K = 4864 the register-staged kernel's split-K is faster (13.3 against 19.7).
+    const bool kw_q_ok = (MODE == B_Q8K || MODE == B_Q4K) && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 &&
+                         avec && (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w && path != 1;
+    if (kw_q_ok) {
+        constexpr int QBM = MODE == B_Q8K ? 8 : 4;
+        const int kq = path == 4 ? (g_ov_bm.load() == 64 ? 64 : 32) : (path == 0 && p.K <= 3072 ? kw_auto(p.M, p.N) : 0);
         if (kq == 64) {
-            HX_LAUNCH((gemm_nk_kw<64, false, false, true>), dim3((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64)),
+            HX_LAUNCH((gemm_nk_kw<64, false, false, QBM>), dim3((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64)),
                       dim3(TPB), 0, p);
             return;
         }
         if (kq == 32) {
-            HX_LAUNCH((gemm_nk_kw<32, false, false, true>), dim3((unsigned) ((p.N + 31) / 32), (unsigned) ((p.M + 31) / 32)),
+            HX_LAUNCH((gemm_nk_kw<32, false, false, QBM>), dim3((unsigned) ((p.N + 31) / 32), (unsigned) ((p.M + 31) / 32)),
                       dim3(TPB), 0, p);
             return;
         }

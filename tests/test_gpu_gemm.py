@@ -713,3 +713,40 @@ def test_q8k_kw_path(dev, tile, M, Kd, N, act):
     np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
     assert K.close_f16(got, dev.down(d3), 0.01, 3e-4).all()
     assert K.close_f16(got, K.matmul_q8k(a, wq, bias, Kd, N, act), 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("tile", [32, 64])
+@pytest.mark.parametrize("M,Kd,N,act", [(16, 4864, 896, 0), (1, 2048, 2048, 0), (256, 768, 2304, 1), (70, 512, 100, 2)])
+def test_q4k_kw_path(dev, tile, M, Kd, N, act):
+    """K-grouped q4_0 weights on the K-across-waves kernel (forced with path 4,
+    whatever K; automatic up to K = 3072; BASELINE cfg 5's 4864 x 896 and
+    2048 x 2048 at M 1 and 16): bit-identical
+    to the same kernel on the fp16 W^T they dequantize to (fp16(d * (q - 8))),
+    and within the harness tolerance of the register-staged q4 kernel and the
+    oracle."""
+    from oracle.quant import dequantize_q4_0_fp16
+    r = rng(28)
+    n_blocks = N * Kd // 32
+    blocks = np.empty((n_blocks, 18), np.uint8)
+    blocks[:, :2] = r.uniform(0.005, 0.02, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = r.integers(0, 256, (n_blocks, 16), dtype=np.uint8)
+    wq = blocks.tobytes()
+    wt16 = h16(dequantize_q4_0_fp16(wq, (N, Kd)))
+    a = h16(r.standard_normal((M, Kd)))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dq, dwt, db = dev.up(a), dev.up(blocks), dev.up(np.ascontiguousarray(wt16)), dev.up(bias)
+    d1, d2, d3 = (dev.empty((M, N), np.float16) for _ in range(3))
+    bm = 64 if tile == 64 else 0
+    try:
+        assert dev.lib.hexlib_gpu_gemm_override(bm, bm, 0, 4) == 1
+        dev.lib.matmul_epilogue_q4k_fp16(dev.ptr(da), dev.ptr(dq), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dwt), dev.ptr(db), dev.ptr(d2), M, Kd, N, act)
+        assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 1) == 1
+        dev.lib.matmul_epilogue_q4k_fp16(dev.ptr(da), dev.ptr(dq), dev.ptr(db), dev.ptr(d3), M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    got = dev.down(d1)
+    np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
+    assert K.close_f16(got, dev.down(d3), 0.01, 3e-4).all()
+    assert K.close_f16(got, K.matmul_q4k(a, wq, bias, Kd, N, act), 0.01, 3e-4).all()
