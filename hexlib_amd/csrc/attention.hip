@@ -109,7 +109,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     // ds_read_b128 phase reads in distinct banks
     constexpr int K_STRIDE = D + 8;
     __shared__ __attribute__((aligned(16))) f16 k_all[WAVES][KT * K_STRIDE];
-    __shared__ float part_o[WAVES][QT][D + 1];
+    // partial outputs, rows padded by 4 floats: 16-byte writes and reads, and the
+    // 16 rows of one ds_write_b128 phase fall in distinct 16-byte bank groups
+    constexpr int PO_STRIDE = D + 4;
+    __shared__ __attribute__((aligned(16))) float part_o[WAVES][QT][PO_STRIDE];
     __shared__ float part_m[WAVES][QT], part_l[WAVES][QT];
 
     const int bh = blockIdx.y;
@@ -245,8 +248,9 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            part_o[wave][c32][32 * t + (i >> 2) * 8 + 4 * hl + (i & 3)] = oacc[t][i];
+        for (int i4 = 0; i4 < 4; ++i4)
+            *reinterpret_cast<f32x4 *>(&part_o[wave][c32][32 * t + i4 * 8 + 4 * hl]) =
+                f32x4{oacc[t][4 * i4], oacc[t][4 * i4 + 1], oacc[t][4 * i4 + 2], oacc[t][4 * i4 + 3]};
     __syncthreads();
 
     // 32 queries x D outputs, 8 consecutive d per thread
@@ -262,8 +266,13 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
         for (int w = 0; w < WAVES; ++w) {
             const float a = exp2f(part_m[w][qq] - mx);   // 0 for a wave that saw no key
             wsum += a * part_l[w][qq];
+            const f32x4 o0 = *reinterpret_cast<const f32x4 *>(&part_o[w][qq][d0]);
+            const f32x4 o1 = *reinterpret_cast<const f32x4 *>(&part_o[w][qq][d0 + 4]);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] += a * part_o[w][qq][d0 + j];
+            for (int j = 0; j < 4; ++j) {
+                acc[j] += a * o0[j];
+                acc[j + 4] += a * o1[j];
+            }
         }
         const float inv = 1.0f / wsum;
         f16x8 out;
