@@ -46,6 +46,7 @@ struct RowRegs {
         }
     }
 
+    // f(value, ch, j) gives element j of chunk ch, in fp32.
     template <class F>
     __device__ __forceinline__ void store(f16 *yr, int lane, F f) const {
 #pragma unroll
@@ -55,15 +56,38 @@ struct RowRegs {
             if constexpr (VEC == 8) {
                 f16x8 t;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) t[j] = (f16) f(v[ch][j], base + j);
+                for (int j = 0; j < 8; ++j) t[j] = (f16) f(v[ch][j], ch, j);
                 *reinterpret_cast<f16x8 *>(yr + base) = t;
             } else if constexpr (VEC == 4) {
                 f16x4 t;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) t[j] = (f16) f(v[ch][j], base + j);
+                for (int j = 0; j < 4; ++j) t[j] = (f16) f(v[ch][j], ch, j);
                 *reinterpret_cast<f16x4 *>(yr + base) = t;
             } else {
-                yr[base] = (f16) f(v[ch][0], base);
+                yr[base] = (f16) f(v[ch][0], ch, 0);
+            }
+        }
+    }
+};
+
+// Per-column parameters (LayerNorm/RMSNorm weight and bias) for the lane's
+// elements, in the RowRegs order. Loaded together with the row, so their
+// memory latency overlaps the row's instead of following the reductions.
+// A chunk past the row end holds zeros and is never used.
+template <int VEC, int NCH, class T>
+struct ColRegs {
+    T v[NCH][VEC];
+
+    __device__ __forceinline__ void load(const T *__restrict__ p, const bool (&ok)[NCH], int lane) {
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            const int base = (ch * HX_WAVE + lane) * VEC;
+            if (ok[ch]) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[ch][j] = p[base + j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[ch][j] = T(0);
             }
         }
     }
@@ -93,7 +117,7 @@ __global__ __launch_bounds__(TPB) void softmax_regs(const f16 *__restrict__ x, f
             s += e;
         }
     s = wave_sum(s);
-    r.store(y + row * C, lane, [s](float e, int) { return e / s; });
+    r.store(y + row * C, lane, [s](float e, int, int) { return e / s; });
 }
 
 template <int VEC, int NCH>
@@ -106,9 +130,13 @@ __global__ __launch_bounds__(TPB) void layernorm_regs(const f16 *__restrict__ x,
     if (row >= R) return;
     RowRegs<VEC, NCH> r;
     r.load(x + row * C, C, lane, 0.0f);
+    ColRegs<VEC, NCH, float> wr, br;
+    wr.load(w, r.ok, lane);
+    br.load(b, r.ok, lane);
     float mean, inv;
     ln_row_stats<VEC, NCH>(r.v, r.ok, C, eps, mean, inv);
-    r.store(y + row * C, lane, [=](float d, int c) { return ln_apply(d, inv, w[c], b[c]); });
+    r.store(y + row * C, lane,
+            [&](float d, int ch, int j) { return ln_apply(d, inv, wr.v[ch][j], br.v[ch][j]); });
 }
 
 template <int VEC, int NCH>
@@ -120,13 +148,15 @@ __global__ __launch_bounds__(TPB) void rmsnorm_regs(const f16 *__restrict__ x,
     if (row >= R) return;
     RowRegs<VEC, NCH> r;
     r.load(x + row * C, C, lane, 0.0f);
+    ColRegs<VEC, NCH, f16> wr;
+    wr.load(w, r.ok, lane);
     float q = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
         for (int j = 0; j < VEC; ++j) q += r.v[ch][j] * r.v[ch][j];
     const float inv = 1.0f / sqrtf(wave_sum(q) / (float) C + eps);
-    r.store(y + row * C, lane, [=](float v, int c) { return v * inv * (float) w[c]; });
+    r.store(y + row * C, lane, [&](float v, int ch, int j) { return v * inv * (float) wr.v[ch][j]; });
 }
 
 // ---- rows too wide for registers: re-read x from memory ------------------------
