@@ -1927,6 +1927,71 @@ void launch_lds_rope(const GemmArgs &p, Tile t) {
     else HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, true>), grid, dim3(TPB), 0, p);
 }
 
+// Few-row GEMM on K-grouped quantized weights (QB = 4: q4_0, 18-byte blocks;
+// QB = 8: q8_0, 34-byte blocks): one wave per output column n. The wave's
+// lanes walk the K/32 blocks of row n of W^T (one contiguous run of bytes),
+// dequantize each weight as the tiled kernels do, fp16(d * (q - 8)) or
+// fp16(d * q), and multiply it by A's rows in fp32 (the fp16 x fp16 product is
+// exact in fp32, as in the MFMA); an xor-butterfly sums the lanes. Up to
+// GEMV_M rows: there a 32-row MFMA tile is mostly empty and the launch is
+// bound by the weight stream. Needs K % 32 == 0, A rows 16-byte aligned.
+constexpr int GEMV_M = 4;
+
+template <int QB>
+__global__ __launch_bounds__(TPB) void gemv_q(GemmArgs p) {
+    constexpr int BLK = QB == 4 ? 18 : 34;
+    const int lane = threadIdx.x & (HX_WAVE - 1);
+    const int n = blockIdx.x * (TPB / HX_WAVE) + (threadIdx.x >> 6);
+    if (n >= p.N) return;
+    const uint8_t *W = static_cast<const uint8_t *>(p.B) + (long long) n * p.ldb;
+    const int kb_n = p.K / 32;
+    float acc[GEMV_M] = {};
+    for (int kb = lane; kb < kb_n; kb += HX_WAVE) {
+        f16 w[32];
+        if constexpr (QB == 4) {
+            float d;
+            uint32_t qs[4];
+            load_q4_block(W + (long long) kb * BLK, d, qs);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                w[j] = q4_val(d, nib(qs, j, 0));
+                w[j + 16] = q4_val(d, nib(qs, j, 4));
+            }
+        } else {
+            float d;
+            uint32_t q0[4], q1[4];
+            load_q8_half(W + (long long) kb * BLK, 0, d, q0);
+            load_q8_half(W + (long long) kb * BLK, 1, d, q1);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                w[j] = q8_val(d, q0, j);
+                w[j + 16] = q8_val(d, q1, j);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < GEMV_M; ++m) {
+            if (m >= p.M) break;
+            const f16x8 *a = reinterpret_cast<const f16x8 *>(p.A + (long long) m * p.lda + kb * 32);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f16x8 x = a[c];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[m] += (float) w[c * 8 + j] * (float) x[j];
+            }
+        }
+    }
+    const float bias = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+    for (int m = 0; m < GEMV_M; ++m) {
+        if (m >= p.M) break;
+        const float v = wave_sum(acc[m]);
+        if (lane == 0) {
+            const f16 r = p.R ? p.R[(long long) m * p.ldr + n] : (f16) 0;
+            p.C[(long long) m * p.ldc + n] = epi(v + bias, p.act, p.R, r);
+        }
+    }
+}
+
 // The LayerNorm-prologue form: 64x64 tiles, one split (every workgroup reads
 // its whole A row block anyway).
 void launch_ln(const GemmArgs &p) {
@@ -1975,6 +2040,19 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     // kernel). Up to K = 3072 (a sweep on MI355X: 256 x 768 x 2304 q8_0 8.2 us
     // against 12.0, cfg 5's 2048 x 2048 q4_0 at M = 1 10.0 against 12.1); at
     // K = 4864 the register-staged kernel's split-K is faster (13.3 against 19.7).
+    // q8_0 and K-grouped q4_0 weights at a few rows: one wave per output column
+    // (automatic route only; the forced paths keep their kernels). Measured on
+    // MI355X at M = 1, q4_0: 896 x 4864 4.5 us against 13.5, 2048 x 2048 3.5
+    // against 10.0; at M = 4 it is still ahead for K >= 896 (896 x 4864 8.5
+    // against 13.6) and behind at K = 768 (5.9 against 5.4).
+    if constexpr (MODE == B_Q8K || MODE == B_Q4K) {
+        if (path == 0 && batch == 1 && (p.M <= 2 || (p.M <= GEMV_M && p.K >= 896)) && p.K % 32 == 0 &&
+            p.lda % 8 == 0 && avec && !p.rcos && !p.ln_w) {
+            constexpr int WPB = TPB / HX_WAVE;
+            HX_LAUNCH((gemv_q<MODE == B_Q8K ? 8 : 4>), dim3((unsigned) ((p.N + WPB - 1) / WPB)), dim3(TPB), 0, p);
+            return;
+        }
+    }
     const bool kw_q_ok = (MODE == B_Q8K || MODE == B_Q4K) && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 &&
                          avec && (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w && path != 1;
     if (kw_q_ok) {

@@ -446,14 +446,15 @@ def test_matmul_q8k(dev, M, Kd, N, act):
     assert K.close_f16(got, want, 0.01, 3e-4).all()
 
 
-def test_q8k_is_the_f16_gemm_on_its_dequantized_weight(dev):
+@pytest.mark.parametrize("M", [64, 2])
+def test_q8k_is_the_f16_gemm_on_its_dequantized_weight(dev, M):
     """A q8_0 weight with d = 1 in every block and integer codes dequantizes
     to those integers exactly; with activations on a quarter grid every
     partial sum is exact in fp32, so the kernel's output is the exact product
-    rounded once to fp16."""
+    rounded once to fp16 (M = 2: the one-wave-per-column kernel)."""
     from hexlib_amd.quant import quantize_q8_0
     r = rng(10)
-    M, Kd, N = 64, 256, 96
+    Kd, N = 256, 96
     w = r.integers(-127, 128, (Kd, N)).astype(np.float32)
     w[::32, :] = 127.0                               # amax 127 in every block along K -> d = 1
     wq = quantize_q8_0(np.ascontiguousarray(w.T))
@@ -713,6 +714,39 @@ def test_q8k_kw_path(dev, tile, M, Kd, N, act):
     np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
     assert K.close_f16(got, dev.down(d3), 0.01, 3e-4).all()
     assert K.close_f16(got, K.matmul_q8k(a, wq, bias, Kd, N, act), 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("qb", [4, 8])
+@pytest.mark.parametrize("M,Kd,N,act", [(1, 896, 4864, 0), (1, 4864, 896, 0), (1, 2048, 2048, 1), (3, 1024, 100, 2),
+                                        (4, 4864, 896, 1), (2, 96, 5, 0), (2, 768, 3072, 1)])
+def test_gemv_quantized_path(dev, qb, M, Kd, N, act):
+    """q4_0 (K-grouped) and q8_0 weights at up to 2 rows (4 with K >= 896)
+    take the one-wave-per-column kernel on the automatic route (BASELINE cfg
+    5's shapes at M = 1, K % 256 != 0, ragged N): within the harness tolerance
+    of the oracle and of the register-staged kernel (path 1)."""
+    r = rng(29 + qb)
+    blk = 18 if qb == 4 else 34
+    n_blocks = N * Kd // 32
+    blocks = np.empty((n_blocks, blk), np.uint8)
+    blocks[:, :2] = r.uniform(0.005, 0.02, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = r.integers(0, 256, (n_blocks, blk - 2), dtype=np.uint8)
+    wq = blocks.tobytes()
+    a = h16(r.standard_normal((M, Kd)))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dq, db = dev.up(a), dev.up(blocks), dev.up(bias)
+    d1, d2 = (dev.empty((M, N), np.float16) for _ in range(2))
+    fn = dev.lib.matmul_epilogue_q4k_fp16 if qb == 4 else dev.lib.matmul_epilogue_q8k_fp16
+    try:
+        fn(dev.ptr(da), dev.ptr(dq), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+        assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 1) == 1
+        fn(dev.ptr(da), dev.ptr(dq), dev.ptr(db), dev.ptr(d2), M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    got = dev.down(d1)
+    want = K.matmul_q4k(a, wq, bias, Kd, N, act) if qb == 4 else K.matmul_q8k(a, wq, bias, Kd, N, act)
+    assert K.close_f16(got, want, 0.01, 3e-4).all()
+    assert K.close_f16(got, dev.down(d2), 0.01, 3e-4).all()
 
 
 @pytest.mark.parametrize("tile", [32, 64])
