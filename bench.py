@@ -318,6 +318,69 @@ def suite_cases():
     ]
 
 
+def q4_gemm_sweep(reps: int = 20) -> list[dict]:
+    """BASELINE cfg 5: the K-grouped q4_0 GEMM (`matmul_epilogue_q4k_fp16`,
+    fp16 scales U(0.005, 0.02), uniform nibbles, A ~ N(0, 1), no bias) at
+    M in {1, 16, 256} and K x N in {896 x 4864, 4864 x 896, 2048 x 2048}.
+    Each figure is the mean launch time over a captured graph of `reps`
+    launches on one set of buffers (cache-warm), best of 5 replays."""
+    import ctypes
+    import torch
+    from hexlib_amd import lib as L
+    lib = L.load()
+    P = ctypes.c_void_p
+    stream = lambda: lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+    r = np.random.default_rng(5)
+    rows = []
+    for M in (1, 16, 256):
+        for Kd, N in ((896, 4864), (4864, 896), (2048, 2048)):
+            nb = N * Kd // 32
+            blocks = np.empty((nb, 18), np.uint8)
+            blocks[:, :2] = r.uniform(0.005, 0.02, nb).astype(np.float16).view(np.uint8).reshape(-1, 2)
+            blocks[:, 2:] = r.integers(0, 256, (nb, 16), dtype=np.uint8)
+            wq = torch.from_numpy(blocks.reshape(-1)).cuda()
+            a = torch.from_numpy(r.standard_normal((M, Kd)).astype(np.float16)).cuda()
+            bias = torch.zeros(N, dtype=torch.float32, device="cuda")
+            c = torch.empty(M, N, dtype=torch.float16, device="cuda")
+            call = lambda: lib.matmul_epilogue_q4k_fp16(P(a.data_ptr()), P(wq.data_ptr()), P(bias.data_ptr()),
+                                                        P(c.data_ptr()), M, Kd, N, 0)
+            stream()
+            call()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                stream()
+                for _ in range(reps):
+                    call()
+            stream()
+            g.replay()
+            torch.cuda.synchronize()
+            best = float("inf")
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                best = min(best, e0.elapsed_time(e1) * 1e6 / reps)
+            del g
+            if lib.hexlib_gpu_take_error() != 0:
+                raise RuntimeError(f"q4 GEMM {M}x{Kd}x{N} reported an error")
+            nbytes = nb * 18 + M * Kd * 2 + N * 4 + M * N * 2
+            flops = 2.0 * M * Kd * N
+            mfma = flops / nbytes > MFMA_FP16_PEAK_TFLOPS * 1e3 / HBM_PEAK_GBS
+            rate = flops / best / 1e3 if mfma else nbytes / best
+            peak = MFMA_FP16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS
+            row = {"shape": [M, Kd, N], "avg_ns": round(best, 1), "bound": "mfma" if mfma else "hbm",
+                   "achieved": round(rate, 3 if mfma else 1), "unit": "TFLOP/s" if mfma else "GB/s",
+                   "frac": round(rate / peak, 4), "algorithmic_bytes": nbytes}
+            rows.append(row)
+            log(f"cfg5 q4 {M}x{Kd}x{N}: {best:.0f} ns, {row['achieved']} {row['unit']} ({row['frac']*100:.1f}%)")
+    torch.cuda.synchronize()
+    lib.hexlib_gpu_set_stream(P(None))
+    return rows
+
+
 def suite(session, min_footprint=600 << 20, max_reps=400) -> list[dict]:
     import torch
     from hexlib_amd.exec import wire
@@ -522,6 +585,7 @@ def main() -> int:
                 variants[label] = {"error": f"{type(e).__name__}: {e}"}
 
     suite_rows = [] if args.no_suite else suite(session)
+    q4_rows = [] if args.no_suite else q4_gemm_sweep()
 
     cpu = None
     if not args.no_cpu:
@@ -542,6 +606,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "per_op_in_plan": per_op,
         "per_op_suite_cold": suite_rows,
+        "q4_gemm_cfg5": q4_rows,
         "variants": variants,
     }
     session.close()
