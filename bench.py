@@ -94,7 +94,9 @@ def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True, laye
     LayerNorm into the linear it feeds) is off: every workgroup of that
     kernel normalises its whole row block again, 48 times per row at fc1,
     which costs more than the separate launch it saves (18.6 us against
-    9.4 + 2.5 us on MI355X)."""
+    9.4 + 2.5 us on MI355X; a K-across-waves form with the row block resident
+    measured 15.9 us, its LDS reads of the row spread over 8 KB slices
+    conflicting 8 ways)."""
     from hexlib_amd import encoder as E
     from hexlib_amd.exec.wholeplan import build_whole_plan_batch
     g = E.build_vision_encoder(cfg)
@@ -381,7 +383,71 @@ def q4_gemm_sweep(reps: int = 20) -> list[dict]:
     return rows
 
 
-def suite(session, min_footprint=600 << 20, max_reps=400) -> list[dict]:
+def q4n_gemm_rows(reps: int = 20) -> list[dict]:
+    """The reference-ABI q4_0 GEMM (`matmul_epilogue_fp16`: q4_0 blocks of 32
+    along N, `kernels/matmul_epilogue_fp16/kernel_api.h:68-109,188-190`) at
+    the encoder's four linear shapes at batch 1 (M = 256), with the bias and
+    activation of each linear. Weights from quantize_q4_0 of N(0, 0.02);
+    activations N(0, 1). Mean launch time over a captured graph of `reps`
+    launches on one buffer set (cache-warm), best of 5 replays; roofline by
+    the shape's arithmetic intensity (q4_0 weight bytes K * N * 18 / 32)."""
+    import ctypes
+    import torch
+    from hexlib_amd import lib as L
+    from hexlib_amd.quant import pack_q4_0_nblocked
+    lib = L.load()
+    P = ctypes.c_void_p
+    r = np.random.default_rng(7)
+    rows = []
+    for Kd, N, act in ((768, 2304, 0), (768, 768, 0), (768, 3072, 1), (3072, 768, 0)):
+        M = 256
+        w = pack_q4_0_nblocked((r.standard_normal((Kd, N)) * 0.02).astype(np.float32))
+        wq = torch.frombuffer(bytearray(w), dtype=torch.uint8).cuda()
+        a = torch.from_numpy(r.standard_normal((M, Kd)).astype(np.float16)).cuda()
+        bias = torch.from_numpy((r.standard_normal(N) * 0.02).astype(np.float32)).cuda()
+        c = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        call = lambda: lib.matmul_epilogue_fp16(P(a.data_ptr()), P(wq.data_ptr()), P(bias.data_ptr()),
+                                                P(c.data_ptr()), M, Kd, N, act)
+        lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+        call()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+            for _ in range(reps):
+                call()
+        lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+        g.replay()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e6 / reps)
+        del g
+        if lib.hexlib_gpu_take_error() != 0:
+            raise RuntimeError(f"q4_0 GEMM {M}x{Kd}x{N} reported an error")
+        nbytes = len(w) + M * Kd * 2 + N * 4 + M * N * 2
+        flops = 2.0 * M * Kd * N
+        mfma = flops / nbytes > MFMA_FP16_PEAK_TFLOPS * 1e3 / HBM_PEAK_GBS
+        rate = flops / best / 1e3 if mfma else nbytes / best
+        peak = MFMA_FP16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS
+        row = {"op": "matmul_epilogue_fp16 (q4_0 along N)", "shape": [M, Kd, N], "act": act,
+               "avg_ns": round(best, 1), "bound": "mfma" if mfma else "hbm",
+               "achieved": round(rate, 3 if mfma else 1), "unit": "TFLOP/s" if mfma else "GB/s",
+               "frac": round(rate / peak, 4), "tflops": round(flops / best / 1e3, 2),
+               "algorithmic_bytes": nbytes}
+        rows.append(row)
+        log(f"q4_0 (N-blocked) {M}x{Kd}x{N}: {best:.0f} ns, {row['achieved']} {row['unit']} "
+            f"({row['frac'] * 100:.1f}%)")
+    lib.hexlib_gpu_set_stream(P(None))
+    return rows
+
+
+def suite(session, min_footprint=600 << 20, max_reps=4000) -> list[dict]:
     import torch
     from hexlib_amd.exec import wire
     from hexlib_amd.exec.runner import KIND_ID, select
@@ -443,33 +509,205 @@ def suite(session, min_footprint=600 << 20, max_reps=400) -> list[dict]:
     return rows
 
 
+# ---- batch-32 GEMMs against the vendor library ------------------------------------------
+
+def library_matmul_ns(m: int, k: int, n: int, reps: int = 20) -> float:
+    """Mean ns of torch.matmul (hipBLASLt) on the same fp16 shape, A [m,k] times
+    a transposed [n,k] weight, fp32 accumulate, no epilogue: the attainable
+    bar for the product GEMM. A captured graph of `reps` launches timed with
+    events on torch's stream, best of 5 replays."""
+    import torch
+    a = torch.randn(m, k, dtype=torch.float16, device="cuda")
+    w = torch.randn(n, k, dtype=torch.float16, device="cuda").mul_(0.02)
+    out = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    torch.matmul(a, w.t(), out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            torch.matmul(a, w.t(), out=out)
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e6 / reps)
+    del g
+    return best
+
+
+def plain_linear_ns(m: int, k: int, n: int, act: int = 0, reps: int = 20) -> float:
+    """Mean ns of this library's matmul_epilogue_f16wt_fp16 (no residual, no
+    rope) on one fp16 shape with torch-allocated operands: a captured graph of
+    `reps` launches on torch's stream, best of 5 replays."""
+    import ctypes
+    import torch
+    from hexlib_amd import lib as L
+    lib = L.load()
+    P = ctypes.c_void_p
+    a = torch.randn(m, k, dtype=torch.float16, device="cuda")
+    wt = torch.randn(n, k, dtype=torch.float16, device="cuda").mul_(0.02)
+    bias = torch.zeros(n, dtype=torch.float32, device="cuda")
+    out = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    call = lambda: lib.matmul_epilogue_f16wt_fp16(P(a.data_ptr()), P(wt.data_ptr()), P(bias.data_ptr()),
+                                                  P(out.data_ptr()), m, k, n, act)
+    lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+    call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+        for _ in range(reps):
+            call()
+    lib.hexlib_gpu_set_stream(P(torch.cuda.current_stream().cuda_stream))
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e6 / reps)
+    del g
+    if lib.hexlib_gpu_take_error() != 0:
+        raise RuntimeError(f"linear {m}x{k}x{n} reported an error")
+    lib.hexlib_gpu_set_stream(P(None))
+    return best
+
+
+def gemm_b32(session, reps: int = 20, library: bool = True) -> list[dict]:
+    """The four linears of the cfg-4 product plan at batch 32 (M = 8192), each
+    timed in the plan's own buffers as a captured graph of `reps` launches of
+    the product op (epilogue included), beside torch.matmul on the same shape
+    without an epilogue."""
+    from hexlib_amd import encoder as E
+    from hexlib_amd.exec.gpu import GpuPlan
+    cfg = replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope", batch=32)
+    g, _, wb = build_plan(cfg)
+    plan = GpuPlan(wb, session)
+    rows = []
+    try:
+        for (spec, ins, (oshape, odt)), (count, idx, op) in unique_ops(g, wb).items():
+            if not spec.startswith("matmul_epilogue") or ins[0][0][0] != 32 * cfg.num_tokens:
+                continue
+            m, k = ins[0][0]
+            n = oshape[-1]
+            ns = time_blob(session, repeat_op_blob(wb, idx, reps), reps) / reps
+            flops = 2.0 * m * k * n
+            row = {"op": spec, "shape": [m, k, n], "count": count, "avg_ns": round(ns, 1),
+                   "tflops": round(flops / ns / 1e3, 1),
+                   "frac": round(flops / ns / 1e3 / MFMA_FP16_PEAK_TFLOPS, 4)}
+            if library:
+                lns = library_matmul_ns(m, k, n)
+                row.update({"library_ns": round(lns, 1), "library_tflops": round(flops / lns / 1e3, 1)})
+            if spec != "matmul_epilogue_f16wt":
+                pns = plain_linear_ns(m, k, n)
+                row.update({"plain_linear_ns": round(pns, 1)})
+            rows.append(row)
+            log(f"b32 {spec} {m}x{k}x{n}: {ns:.0f} ns ({row['tflops']} TFLOP/s)"
+                + (f"; torch.matmul {row['library_ns']:.0f} ns ({row['library_tflops']} TFLOP/s)"
+                   if library else ""))
+    finally:
+        plan.close()
+    return rows
+
+
 # ---- CPU baseline ------------------------------------------------------------------------
 
-def cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
+def _cpu_images_per_s(cfg, budget_s: float):
+    """Images/s of the numpy storage-rounding executor (`oracle.eager.run_stored`,
+    the restated `hexlib/exec/interpreter.py:80-205`) on the REFERENCE graph of
+    `cfg` (the unfused attention chain the reference builds), for about
+    `budget_s` seconds of CPU work."""
     from hexlib_amd import encoder as E
     from hexlib_amd.graph.fuse import fuse
     from oracle import eager
-    g = fuse(E.build_vision_encoder(cfg))
-    feeds = E.synthetic_feeds(g, cfg, seed=0)
-    threads = None
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # noqa: BLE001 -- informational only
-        threads = os.cpu_count()
+    ref = replace(cfg, attention="unfused")
+    g = fuse(E.build_vision_encoder(ref))
+    feeds = E.synthetic_feeds(g, ref, seed=0)
     n = 0
     t0 = time.perf_counter()
     while True:
         eager.run_stored(g, feeds)
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
+        if el >= budget_s or n >= 200:
             break
+    return n, el
+
+
+def cpu_per_op(budget_s: float = 0.5) -> list[dict]:
+    """Each cfg-2 / cfg-3 op of the cold suite through the oracle's scalar
+    kernel restatements (`oracle.kernels`, the reference baselines' numerics)
+    on the same inputs: mean ms per call over about `budget_s` seconds."""
+    from oracle import kernels as K
+    from hexlib_amd.quant import pack_q4_0_nblocked
+    rows = []
+    for kind, attrs, arrays, out_shape in suite_cases():
+        if kind == "rmsnorm":
+            fn = lambda: K.rmsnorm_fp16(arrays[0], arrays[1], attrs["eps"])
+        elif kind == "layernorm":
+            fn = lambda: K.layernorm_fp16(arrays[0], arrays[1], arrays[2], attrs["eps"])
+        elif kind == "softmax":
+            fn = lambda: K.softmax_fp16(arrays[0])
+        elif kind == "rope_2d":
+            fn = lambda: K.rope_2d_fp16(*arrays)
+        elif kind == "transpose":
+            fn = (lambda: K.transpose_th_fp16(arrays[0])) if attrs["perm"] == (1, 0, 2) else \
+                 (lambda: K.transpose_hd_fp16(arrays[0]))
+        elif kind == "add":
+            fn = lambda: K.add_fp16(arrays[0], arrays[1])
+        elif kind == "scale":
+            fn = lambda: K.scale_fp16(arrays[0], attrs["factor"])
+        elif kind == "cast":
+            fn = lambda: K.cast_f32_f16(arrays[0])
+        elif kind == "patchify":
+            fn = lambda: K.patchify_fp32(arrays[0], attrs["patch"], attrs["merge"], attrs["grid_h"], attrs["grid_w"])
+        elif kind == "matmul_epilogue":
+            act = {"none": 0, "gelu_tanh": 1, "gelu_erf": 2}[attrs["act"]]
+            fn = lambda: K.matmul_epilogue_f16w(arrays[0], arrays[1], arrays[2], act)
+        elif kind == "matmul":
+            fn = lambda: K.matmul_fp16(arrays[0], arrays[1])
+        else:
+            continue
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or n >= 1000:
+                break
+        rows.append({"op": kind, "shape": [list(a.shape) for a in arrays], "ms": round(el / n * 1e3, 3)})
+    return rows
+
+
+def cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
+    """The CPU baseline: the reference graph of the headline encoder through
+    the numpy executor on this host's cores (the headline figure), plus the
+    cfg-1 tiny encoder and the cfg-2 / cfg-3 ops, each timed briefly."""
+    from hexlib_amd import encoder as E
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001 -- informational only
+        threads = os.cpu_count()
+    n, el = _cpu_images_per_s(cfg, budget_s)
+    n1, el1 = _cpu_images_per_s(E.TINY_ENCODER, 2.0)
     return {"value": round(n / el, 4), "unit": "images/s", "cores": int(threads or 1),
             "kind": "port",
-            "sample": f"{n} image(s) of the cfg-4 256x256 encoder through the numpy oracle "
-                      f"(storage-rounding interpreter restatement) in {el:.1f} s; "
-                      f"os.cpu_count()={os.cpu_count()}, numpy {np.__version__}"}
+            "sample": f"{n} image(s) of the cfg-4 256x256 encoder's reference graph (259 ops, unfused "
+                      f"attention) through the numpy oracle (storage-rounding interpreter restatement) "
+                      f"in {el:.1f} s; os.cpu_count()={os.cpu_count()}, numpy {np.__version__}",
+            "cfg1_tiny_encoder_images_per_s": round(n1 / el1, 2),
+            "per_op_ms": cpu_per_op()}
 
 
 def run_variant(session, vcfg, steps: int, label: str) -> dict:
@@ -511,6 +749,10 @@ def main() -> int:
                     help="build the plan, launch only the dominant kernel (and, with --copy-ref, a "
                          "plain copy of known size) and print its roofline object")
     ap.add_argument("--copy-ref", action="store_true")
+    ap.add_argument("--gemm-b32", action="store_true",
+                    help="time the four batch-32 product linears in the plan and torch.matmul on the "
+                         "same shapes, print them and exit (the rocprofv3 --pmc target for those GEMMs)")
+    ap.add_argument("--no-library", action="store_true", help="with --gemm-b32: skip torch.matmul")
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 output directory and exit")
     args = ap.parse_args()
@@ -528,6 +770,11 @@ def main() -> int:
     from hexlib_amd.exec.gpu import GpuPlan, GpuSession
 
     session = GpuSession()
+    if args.gemm_b32:
+        rows = gemm_b32(session, library=not args.no_library)
+        session.close()
+        print(json.dumps({"gemm_b32": rows}))
+        return 0
     cfg = replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
     log("building cfg-4 plan (256x256, batch 1, fused q/k/v linear, q/k rope, fused attention)")
     g, feeds, wb = build_plan(cfg)
@@ -576,6 +823,9 @@ def main() -> int:
                                     max(10, args.steps // 2)),
                                    ("256_b1_reference_graph", E.QWEN35_VISION_FP16, max(10, args.steps // 2)),
                                    ("256_b1_q8_0", replace(E.QWEN35_VISION_Q8, attention="fused_qkv_rope"),
+                                    max(10, args.steps // 2)),
+                                   ("256_b1_q4_0_reference_config",
+                                    replace(E.QWEN35_VISION_Q4, attention="fused_qkv_rope"),
                                     max(10, args.steps // 2))):
             log(f"variant {label}")
             try:
@@ -586,6 +836,7 @@ def main() -> int:
 
     suite_rows = [] if args.no_suite else suite(session)
     q4_rows = [] if args.no_suite else q4_gemm_sweep()
+    q4n_rows = [] if args.no_suite else q4n_gemm_rows()
 
     cpu = None
     if not args.no_cpu:
@@ -607,6 +858,7 @@ def main() -> int:
         "per_op_in_plan": per_op,
         "per_op_suite_cold": suite_rows,
         "q4_gemm_cfg5": q4_rows,
+        "q4_0_reference_abi_gemm": q4n_rows,
         "variants": variants,
     }
     session.close()

@@ -31,6 +31,12 @@ CFLAGS = [
 ]
 
 
+# Per-source flags. attention.hip: MFMA accumulators in VGPRs -- its kernels
+# rescale and read the accumulators with VALU code every key tile, and the
+# AGPR form spent ~250 accvgpr moves per loop and an occupancy step on it.
+EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 class BuildError(RuntimeError):
     pass
 
@@ -40,25 +46,37 @@ def sources() -> list[str]:
                   if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src: str) -> str:
+def _headers_mtime() -> float:
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    hs += [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
+    return max(os.path.getmtime(h) for h in hs)
+
+
+def _compile(src: str, changed_only: bool = False) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+    if changed_only and os.path.exists(obj) and \
+            os.path.getmtime(obj) > max(os.path.getmtime(src), _headers_mtime()):
+        return obj
     # .cpp files hold host code only (runtime, generated entries): no device pass.
     host_only = ["--offload-host-only"] if src.endswith(".cpp") else []
-    cmd = [HIPCC, *CFLAGS, *host_only, "-c", src, "-o", obj]
+    extra = EXTRA_FLAGS.get(os.path.basename(src), [])
+    cmd = [HIPCC, *CFLAGS, *extra, *host_only, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise BuildError(f"compile failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, changed_only: bool = False) -> str:
+    """Compile every source (or, with `changed_only`, those newer than their
+    object or any header) and link the library."""
     from hexlib_amd.exec import genentry
 
     genentry.write()
     os.makedirs(BUILD_DIR, exist_ok=True)
     jobs = max(1, min(len(sources()), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(_compile, sources()))
+        objs = list(pool.map(lambda src: _compile(src, changed_only), sources()))
     tmp = LIB_PATH + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -89,5 +107,5 @@ def build_replay() -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, changed_only="--changed" in sys.argv[1:])
     sys.exit(0)

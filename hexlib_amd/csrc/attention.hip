@@ -10,8 +10,9 @@
 // [rows, 2, H, D] tensor (rope_2d_qk_fp16's output) and v from the fused
 // [rows, 3, H, D] projection, by row stride.
 //
-// Numerics: q.k in fp32 (MFMA accumulate), scaled in fp32; a running max and
-// sum per query (online softmax, exp2 of log2e-scaled scores); the unnormalised
+// Numerics: q.k in fp32 (MFMA accumulate), scaled in fp32 inside the exponent;
+// a running max and sum per query (online softmax, exp2 of log2e-scaled
+// scores, the max raised lazily: see softmax_step); the unnormalised
 // probabilities are rounded to fp16 for the P.V product, accumulated in fp32;
 // the output is divided by the fp32 sum and rounded to fp16 once.
 //
@@ -42,6 +43,7 @@
 // wave complete in order, so the wave-private tile needs no
 // barrier; the only workgroup barrier is before the merge, which every wave
 // reaches.
+#include <atomic>
 #include <cmath>
 
 #include "device.h"
@@ -91,6 +93,71 @@ __device__ __forceinline__ void load_tile(const f16 *__restrict__ kb, long long 
         // keys past T load as zero: their p is 0, and 0 * garbage could be NaN
         t.v[i] = vkey < T ? *reinterpret_cast<const f16x8 *>(vb + vkey * ldv + (e % VCH) * 8) : f16x8{};
     }
+}
+
+// One online-softmax update over NSUB 32-key sub-tiles of scores S^T (element
+// i of sub-tile u is key key0 + 32 u + 16 (i / 8) + 8 hl + i % 8; the lane's
+// query is shared with lane ^ 32). Scores are scaled by c = scale * log2(e)
+// inside the exponent (one fma: exp2(c s - m)), so the running maximum is
+// kept on the scaled scale: m is the reference every p and the partial O are
+// relative to. It is raised only when some query of the wave sees a scaled
+// score more than 8 above it (a wave-uniform branch): until then the
+// probabilities are at most 2^8, far inside fp16 and fp32, and the rescale of
+// O (and its exp2) is skipped. Keys past T are masked only on the sequence's
+// last, partial tile. exp2 is the hardware's v_exp_f32 (about 1 ulp; the
+// probabilities are then rounded to fp16).
+template <int NSUB>
+__device__ __forceinline__ void softmax_step(f32x16 (&s)[NSUB], int key0, int T, float c, int hl, float &m,
+                                             float &l, f32x16 *oacc, int dt, f16x8 (&pb)[NSUB][2]) {
+    // a key past T never wins the extreme and gets p = 0 (set after the exp2:
+    // at c == 0 an infinite score would make it NaN)
+    const bool part = key0 + 32 * NSUB > T;
+    const float pad = c > 0.0f ? -INFINITY : (c < 0.0f ? INFINITY : 0.0f);
+    if (part) {
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = key0 + 32 * u + 16 * (i >> 3) + 8 * hl + (i & 7);
+                if (key >= T) s[u][i] = pad;
+            }
+    }
+    float tmax = -INFINITY;
+    if (c > 0.0f) {
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[u][i]);
+        tmax *= c;
+    } else {
+        float tmin = INFINITY;
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tmin = fminf(tmin, s[u][i]);
+        tmax = tmin * c;
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));      // finite: the tile's first key is valid
+    if (__any(tmax > m + 8.0f)) {
+        const float m_new = fmaxf(m, tmax);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        l *= alpha;
+        for (int t = 0; t < dt; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[t][i] *= alpha;
+        m = m_new;
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][i], c, -m));
+            if (part && key0 + 32 * u + 16 * (i >> 3) + 8 * hl + (i & 7) >= T) p = 0.0f;
+            psum += p;
+            pb[u][i >> 3][i & 7] = (f16) p;
+        }
+    l += psum;
 }
 
 // q and k rows are `ldqk` halves apart, v rows `ldv` (H*D for separate
@@ -198,30 +265,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
         for (int kk = 0; kk < KC; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], s, 0, 0, 0);
 
         // element i of this lane is key kt + 16 (i / 8) + 8 hl + i % 8
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int key = kt + 16 * (i >> 3) + 8 * hl + (i & 7);
-            s[i] = key < T ? s[i] * scale_log2e : -INFINITY;
-            tmax = fmaxf(tmax, s[i]);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m, tmax);     // finite: key kt < T is valid
-        const float alpha = exp2f(m - m_new);
-        f16x8 pb[2];
-        float psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float p = exp2f(s[i] - m_new);
-            psum += p;
-            pb[i >> 3][i & 7] = (f16) p;
-        }
-        l = l * alpha + psum;
-        m = m_new;
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[t][i] *= alpha;
+        f32x16 sv[1] = {s};
+        f16x8 pbv[1][2];
+        softmax_step<1>(sv, kt, T, scale_log2e, hl, m, l, oacc, DT, pbv);
+        const f16x8 pb[2] = {pbv[0][0], pbv[0][1]};
 
 #pragma unroll
         for (int c = 0; c < 2; ++c)
@@ -264,7 +311,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
         float wsum = 0.f, acc[8] = {};
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) {
-            const float a = exp2f(part_m[w][qq] - mx);   // 0 for a wave that saw no key
+            const float a = __builtin_amdgcn_exp2f(part_m[w][qq] - mx);   // 0 for a wave that saw no key
             wsum += a * part_l[w][qq];
             const f32x4 o0 = *reinterpret_cast<const f32x4 *>(&part_o[w][qq][d0]);
             const f32x4 o1 = *reinterpret_cast<const f32x4 *>(&part_o[w][qq][d0 + 4]);
@@ -282,6 +329,231 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     }
 }
 
+// ---- many query tiles per workgroup, K and V shared through LDS -------------
+//
+// attn_fwd gives every wave its own K/V tiles: each (image, head) reads its
+// keys and values once per 32-query tile (8 times at T = 256), a workgroup
+// owns only 32 queries, and the waves merge their partial results at the end.
+// Where the grid is large (many images, or long sequences) this form instead
+// gives a workgroup QG x 32 queries of one (image, head): the QG waves of a
+// key split walk the same 64-key stages, each stage's K and V loaded once
+// (each wave loads 1/QG of it, one stage ahead, into registers) and shared
+// through a two-slot LDS ring, one workgroup barrier per stage. With KS key
+// splits (QG x KS waves) split k takes stages k, k + KS, ... and the splits'
+// (max, sum, O) are merged through LDS at the end, as in attn_fwd; with one
+// split each wave normalises and stores its own queries directly. The per-tile
+// arithmetic (S^T = K Q^T, the online softmax in exp2, fp16 probabilities,
+// O^T = V^T P^T with transpose reads of V) is attn_fwd's; one softmax update
+// covers a 64-key stage.
+constexpr int KS_KEYS = 64;     // keys per stage
+
+template <int D, int QG, int KS>
+__global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ q, const f16 *__restrict__ k,
+                                                        long long ldqk, const f16 *__restrict__ v, long long ldv,
+                                                        f16 *__restrict__ o, int T, int H, float scale_log2e) {
+    constexpr int W = QG * KS;
+    constexpr int KC = D / 16, DT = D / 32, VCH = D / 8;
+    constexpr int V_STRIDE = v_stride<D>(), K_STRIDE = D + 8;
+    constexpr int K_HALVES = KS_KEYS * K_STRIDE, V_HALVES = KS_KEYS * V_STRIDE;
+    constexpr int SLOT = K_HALVES + V_HALVES;                  // one stage of one split
+    constexpr int PIECES = KS_KEYS * VCH / (64 * QG);          // 16-byte pieces per lane per tensor
+    static_assert(KS_KEYS * VCH % (64 * QG) == 0, "the stage splits evenly over the split's waves");
+    constexpr int PO_STRIDE = D + 4;
+    constexpr int RING_BYTES = KS * 2 * SLOT * 2;
+    constexpr int MERGE_BYTES = KS > 1 ? W * 32 * PO_STRIDE * 4 : 0;
+    constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
+    __shared__ __attribute__((aligned(16))) f16 ring[LDS_BYTES / 2];
+    __shared__ float part_m[KS > 1 ? W : 1][32], part_l[KS > 1 ? W : 1][32];
+
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const long long ldo = (long long) H * D, row0 = (long long) b * T;
+    const f16 *qb = q + row0 * ldqk + (long long) h * D, *kb = k + row0 * ldqk + (long long) h * D,
+              *vb = v + row0 * ldv + (long long) h * D;
+    f16 *ob = o + row0 * ldo + (long long) h * D;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
+    const int qg = wave % QG, ks = wave / QG;
+    const int q0 = blockIdx.x * (32 * QG) + qg * 32;
+    const int n_stages = (T + KS_KEYS - 1) / KS_KEYS, iters = (n_stages + KS - 1) / KS;
+    const int tr_off = (8 * hl + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int krow_key = kperm(c32);
+
+    // this lane's pieces of a stage: piece e = qg * 64 + lane + 64 QG i is key e / VCH, chunk e % VCH
+    f16x8 kr[PIECES], vr[PIECES];
+    auto load_stage = [&](int st) {
+        const int key0 = st * KS_KEYS;
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+            const int e = qg * 64 + lane + 64 * QG * i, key = key0 + e / VCH, ch = e % VCH;
+            kr[i] = *reinterpret_cast<const f16x8 *>(kb + (long long) min(key, T - 1) * ldqk + ch * 8);
+            vr[i] = key < T ? *reinterpret_cast<const f16x8 *>(vb + (long long) key * ldv + ch * 8) : f16x8{};
+        }
+    };
+    auto store_stage = [&](int slot) {
+        f16 *kt = ring + (ks * 2 + slot) * SLOT, *vt = kt + K_HALVES;
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+            const int e = qg * 64 + lane + 64 * QG * i, key = e / VCH, ch = e % VCH;
+            *reinterpret_cast<f16x8 *>(kt + key * K_STRIDE + ch * 8) = kr[i];
+            *reinterpret_cast<f16x8 *>(vt + key * V_STRIDE + ch * 8) = vr[i];
+        }
+    };
+
+    // the first stage's loads, then this wave's Q^T operand (query c32, d 16 kk + 8 hl ..)
+    if (ks < n_stages) load_stage(ks);
+    f16x8 qf[KC];
+    {
+        const int qi = min(q0 + c32, T - 1);
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk)
+            qf[kk] = *reinterpret_cast<const f16x8 *>(qb + (long long) qi * ldqk + 16 * kk + 8 * hl);
+    }
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
+    float m = -INFINITY, l = 0.f;
+
+    store_stage(0);
+    __syncthreads();
+    for (int it = 0; it < iters; ++it) {
+        const int st = it * KS + ks, slot = it & 1;
+        const bool live = st < n_stages;
+        if (live && st + KS < n_stages) load_stage(st + KS);   // one stage ahead, into registers
+        if (live) {
+            const f16 *kt = ring + (ks * 2 + slot) * SLOT, *vt = kt + K_HALVES;
+            const int key0 = st * KS_KEYS;
+            f32x16 s[2];
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+                f16x8 kf[KC];
+#pragma unroll
+                for (int kk = 0; kk < KC; ++kk)
+                    kf[kk] = *reinterpret_cast<const f16x8 *>(kt + (32 * sub + krow_key) * K_STRIDE + 16 * kk + 8 * hl);
+                s[sub] = f32x16{};
+#pragma unroll
+                for (int kk = 0; kk < KC; ++kk)
+                    s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], s[sub], 0, 0, 0);
+            }
+            // element i of sub-tile sub is key key0 + 32 sub + 16 (i / 8) + 8 hl + i % 8
+            f16x8 pb[2][2];
+            softmax_step<2>(s, key0, T, scale_log2e, hl, m, l, oacc, DT, pb);
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+                        const f16 *base = vt + tr_off + (32 * sub + 16 * c) * V_STRIDE + 32 * t;
+                        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) v4i16 *) (base));
+                        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) v4i16 *) (base + 4 * V_STRIDE));
+                        const f16x8 va = __builtin_bit_cast(
+                            f16x8, (v8i16){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                        oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[sub][c], oacc[t], 0, 0, 0);
+                    }
+        }
+        // the other slot was last read in the previous iteration: every wave is
+        // past it once this barrier is, so the next stage can land there
+        if (it + 1 < iters) {
+            if (live && st + KS < n_stages) store_stage(slot ^ 1);
+            __syncthreads();
+        }
+    }
+
+    l += __shfl_xor(l, 32);
+    if constexpr (KS == 1) {
+        // this wave owns its queries over every key: O = O^T / l, 4 consecutive d per store
+        const int qi = q0 + c32;
+        if (qi < T) {
+            const float inv = 1.0f / l;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    f16x4 out;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) out[e] = (f16) (oacc[t][4 * i4 + e] * inv);
+                    *reinterpret_cast<f16x4 *>(ob + (long long) qi * ldo + 32 * t + 8 * i4 + 4 * hl) = out;
+                }
+        }
+    } else {
+        // merge the key splits of each query group through LDS (the ring is done)
+        __syncthreads();
+        float *po = reinterpret_cast<float *>(ring);      // [W][32][PO_STRIDE]
+        if (hl == 0) {
+            part_m[wave][c32] = m;
+            part_l[wave][c32] = l;
+        }
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4)
+                *reinterpret_cast<f32x4 *>(po + (wave * 32 + c32) * PO_STRIDE + 32 * t + i4 * 8 + 4 * hl) =
+                    f32x4{oacc[t][4 * i4], oacc[t][4 * i4 + 1], oacc[t][4 * i4 + 2], oacc[t][4 * i4 + 3]};
+        __syncthreads();
+        for (int e = threadIdx.x; e < QG * 32 * (D / 8); e += 64 * W) {
+            const int g = e / (32 * (D / 8)), qq = (e / (D / 8)) % 32, d0 = (e % (D / 8)) * 8;
+            const int qi = blockIdx.x * (32 * QG) + g * 32 + qq;
+            if (qi >= T) continue;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int sp = 0; sp < KS; ++sp) mx = fmaxf(mx, part_m[sp * QG + g][qq]);
+            float wsum = 0.f, acc[8] = {};
+#pragma unroll
+            for (int sp = 0; sp < KS; ++sp) {
+                const int w = sp * QG + g;
+                const float a = __builtin_amdgcn_exp2f(part_m[w][qq] - mx);   // 0 for a split that saw no key
+                wsum += a * part_l[w][qq];
+                const f32x4 o0 = *reinterpret_cast<const f32x4 *>(po + (w * 32 + qq) * PO_STRIDE + d0);
+                const f32x4 o1 = *reinterpret_cast<const f32x4 *>(po + (w * 32 + qq) * PO_STRIDE + d0 + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[j] += a * o0[j];
+                    acc[j + 4] += a * o1[j];
+                }
+            }
+            const float inv = 1.0f / wsum;
+            f16x8 out;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out[j] = (f16) (acc[j] * inv);
+            *reinterpret_cast<f16x8 *>(ob + (long long) qi * ldo + d0) = out;
+        }
+    }
+}
+
+// Tuning override for the attention form (0: automatic; else QG * 10 + KS
+// for attn_qg, or 1 for attn_fwd), set by hexlib_gpu_attention_override.
+std::atomic<int> g_attn_form{0};
+
+// attn_qg with QG query groups and KS key splits; false for a form not built.
+bool launch_qg(int qg, int ks, const f16 *Q, const f16 *K, long long ldqk, const f16 *V, long long ldv, f16 *O,
+               int T, int H, int D, int batch, float sl2e) {
+    const dim3 grid((unsigned) ((T + 32 * qg - 1) / (32 * qg)), (unsigned) (batch * H));
+#define HX_QG(D_, QG_, KS_)                                                                             \
+    if (D == D_ && qg == QG_ && ks == KS_) {                                                            \
+        HX_LAUNCH((attn_qg<D_, QG_, KS_>), grid, dim3(64 * QG_ * KS_), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e); \
+        return true;                                                                                    \
+    }
+    HX_QG(64, 4, 1)
+    HX_QG(64, 2, 1)
+    HX_QG(64, 2, 2)
+    HX_QG(64, 4, 2)
+    HX_QG(32, 4, 1)
+    HX_QG(32, 2, 2)
+#undef HX_QG
+    return false;
+}
+
+// The automatic choice: the shared-K/V form wherever its grid still fills the
+// chip, else 0 (attn_fwd).
+// From a sweep on MI355X (12 heads of 64): 256 tokens at batch 32, 26.6 us
+// against 41.3 (the per-wave-tiles kernel); at 784 and 1024 tokens of one
+// image and at batch 4 the per-wave-tiles kernel is as fast or faster.
+int qg_auto(int T, int H, int batch) {
+    const long long heads = (long long) batch * H;
+    return heads * ((T + 127) / 128) >= 2 * CUS ? 41 : 0;
+}
+
 void launch(const hexlib_hf *q, const hexlib_hf *k, long long ldqk, const hexlib_hf *v, long long ldv,
             hexlib_hf *out, int rows, int H, int D, int batch, float scale) {
     const int T = rows / batch;
@@ -291,6 +563,13 @@ void launch(const hexlib_hf *q, const hexlib_hf *k, long long ldqk, const hexlib
     const auto *K = reinterpret_cast<const f16 *>(k);
     const auto *V = reinterpret_cast<const f16 *>(v);
     auto *O = reinterpret_cast<f16 *>(out);
+    const int form = g_attn_form.load();
+    if (form >= 10) {
+        if (launch_qg(form / 10, form % 10, Q, K, ldqk, V, ldv, O, T, H, D, batch, sl2e)) return;
+    } else if (form == 0) {
+        const int f = qg_auto(T, H, batch);
+        if (f && launch_qg(f / 10, f % 10, Q, K, ldqk, V, ldv, O, T, H, D, batch, sl2e)) return;
+    }
     // Fewer workgroups than CUs (one 256-token image): 8 waves split each
     // query tile's keys, halving every wave's serial chain; otherwise 4, which
     // keeps two workgroups per CU.
@@ -307,6 +586,13 @@ bool dims_ok(int rows, int H, int D, int batch) {
 }
 
 }  // namespace
+
+extern "C" int hexlib_gpu_attention_override(int form) {
+    const bool ok = form == 0 || form == 1 || form == 41 || form == 21 || form == 22 || form == 42;
+    if (!ok) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+    g_attn_form = form;
+    return HEXLIB_DSP_OK;
+}
 
 extern "C" void attention_fp16(const hexlib_hf *q, const hexlib_hf *k, const hexlib_hf *v,
                                hexlib_hf *out, int rows, int H, int D, int batch, float scale) {

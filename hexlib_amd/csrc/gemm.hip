@@ -1355,6 +1355,135 @@ __device__ __forceinline__ void interleave_reads() {
     }
 }
 
+// The rope form's epilogue (BM = BN = 128, rope_d = 64) stages, per pass, the
+// rope tables of the pass's 64 rows in LDS beside the fp32 tile rows: the
+// tables are stored transposed, [rope_d, M], so each table row t holds the
+// pass's rows as two runs of 32 consecutive floats, loaded as 16-byte vectors.
+constexpr int BIG_RD = 64;                     // the rope form's head width
+constexpr int BIG_SLAB_ROW = 64 + 4;           // floats per slab row (one table column t)
+
+// The rope form's epilogue. Per pass i (the 64 tile rows of 32-row block i of
+// both wave rows):
+//  1. the pass's rope tables are loaded as 16-byte vectors (table column t,
+//     4 consecutive rows) and the waves write their fp32 blocks to the staging
+//     rows; the tables go to the slab, [cos | sin][t][row];
+//  2. each thread takes one staged row and four 8-feature output chunks (the
+//     lanes of a wave: 16 rows x 4 consecutive chunks, so a row's stores are
+//     64 contiguous bytes). A rope chunk's 8 output features i .. i + 7 of one
+//     half of a head come from computed columns 2i .. 2i + 15 (the
+//     pair-interleaved weight rows) and table columns t = i .. i + 7 (lo half)
+//     or i + D/2 .. (hi half); a chunk past the rope heads is stored plainly.
+// The arithmetic is rope_store4's (each value rounded to fp16, products and
+// sum rounded separately, rounded again), so the result is bit-identical to
+// the other rope epilogues. Host guarantees: rope_d == 64, M % 4 == 0,
+// 16-byte aligned tables, N % 8 == 0, ldc % 8 == 0, 16-byte aligned C, no
+// residual.
+// The tables of pass i as this thread loads them: table tab's column t = idx / 16
+// at 4 consecutive rows (idx % 16) * 4 of the pass's 64, idx = tid + 256 k.
+// Issued before the K loop (they complete ahead of the ring's copies, which
+// are issued after them), so the epilogue never waits on them.
+template <int BM, int TM>
+__device__ __forceinline__ void big_rope_tables(const GemmArgs &p, int m0, f32x4 (&tv)[TM][2][4]) {
+    const int tid = threadIdx.x;
+    const long long ld = p.M;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int tab = 0; tab < 2; ++tab)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int idx = tid + TPB * k, t = idx >> 4, row4 = (idx & 15) * 4;
+                const int m = m0 + (row4 >> 5) * (BM / 2) + i * 32 + (row4 & 31);
+                const float *src = (tab ? p.rsin : p.rcos) + (long long) t * ld + m;
+                tv[i][tab][k] = m < p.M ? *reinterpret_cast<const f32x4 *>(src) : f32x4{};
+            }
+}
+
+template <int ACT, int BM, int BN, int TM, int TN, int EROW>
+__device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x16 (&acc)[TN][TM], float *stage,
+                                                  int m0, int n0, int wave, int lane, const f32x4 (&tv)[TM][2][4],
+                                                  float bias_own) {
+#pragma clang fp contract(off)
+    constexpr int WN = 2, HALF = BIG_RD / 2;
+    float *slab = stage + 64 * EROW;                       // [2][BIG_RD][BIG_SLAB_ROW]
+    float *bias_s = slab + 2 * BIG_RD * BIG_SLAB_ROW;      // [BN], by output feature
+    const int tid = threadIdx.x, r = lane & 31;
+    // bias by output feature, staged once (visible after the first pass's barrier)
+    if (tid < BN) bias_s[tid] = bias_own;
+    const int row = wave * 16 + (lane & 15);               // this thread's staged row
+    const int cq = lane >> 4;                              // its chunks: cq, cq + 4, cq + 8, cq + 12
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        // 1. staging writes, slab writes
+        __builtin_amdgcn_s_barrier();              // the ring's (or the last pass's) reads are done
+        const int srow = (wave / WN) * 32 + r;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<f32x4 *>(stage + srow * EROW + (wave % WN) * (BN / 2) + j * 32 + g * 8 +
+                                           (lane >> 5) * 4) =
+                    f32x4{acc[j][i][g * 4], acc[j][i][g * 4 + 1], acc[j][i][g * 4 + 2], acc[j][i][g * 4 + 3]};
+#pragma unroll
+        for (int tab = 0; tab < 2; ++tab)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int idx = tid + TPB * k, t = idx >> 4, row4 = (idx & 15) * 4;
+                *reinterpret_cast<f32x4 *>(slab + (tab * BIG_RD + t) * BIG_SLAB_ROW + row4) = tv[i][tab][k];
+            }
+        HX_WAIT_LGKM0();
+        __builtin_amdgcn_s_barrier();
+        // 2. one row, four chunks
+        const int m = m0 + (row >> 5) * (BM / 2) + i * 32 + (row & 31);
+        if (m >= p.M) continue;
+        f16 *crow = p.C + (long long) m * p.ldc;
+        const float *srow_p = stage + row * EROW;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int c = cq + 4 * k, f0 = c * 8, n = n0 + f0;  // output features n .. n + 7
+            if (n >= p.N) continue;
+            f16x8 o;
+            if (n < p.rope_cols) {
+                const int lf = f0 % BIG_RD, hb = f0 - lf;            // feature in head, head start (tile)
+                const bool hi = lf >= HALF;
+                const int i0 = hi ? lf - HALF : lf;                  // pair index of the first feature
+                const float *src = srow_p + hb + 2 * i0;             // computed columns 2 i0 .. 2 i0 + 15
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 a4 = *reinterpret_cast<const f32x4 *>(src + 4 * q);
+                    v[4 * q] = a4[0]; v[4 * q + 1] = a4[1]; v[4 * q + 2] = a4[2]; v[4 * q + 3] = a4[3];
+                }
+                const float *ct = slab + (hi ? lf : i0) * BIG_SLAB_ROW + row;
+                const float *st = ct + BIG_RD * BIG_SLAB_ROW;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    // computed column 2 (i0 + u) is feature i0 + u, 2 (i0 + u) + 1 is feature i0 + u + D/2
+                    const float x0 = (float) (f16) f32_rounded(act_t<ACT>(v[2 * u] + bias_s[hb + i0 + u]));
+                    const float x1 = (float) (f16) f32_rounded(act_t<ACT>(v[2 * u + 1] + bias_s[hb + i0 + u + HALF]));
+                    const float cv = ct[u * BIG_SLAB_ROW], sv = st[u * BIG_SLAB_ROW];
+                    if (hi) {
+                        const float p1 = x1 * cv, q1 = x0 * sv;
+                        o[u] = (f16) f32_rounded(p1 + q1);
+                    } else {
+                        const float p0 = x0 * cv, q0 = x1 * sv;
+                        o[u] = (f16) f32_rounded(p0 - q0);
+                    }
+                }
+            } else {
+                const f32x4 a0 = *reinterpret_cast<const f32x4 *>(srow_p + f0);
+                const f32x4 a1 = *reinterpret_cast<const f32x4 *>(srow_p + f0 + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    o[e] = epi_t<ACT, false>(a0[e] + bias_s[f0 + e], (f16) 0);
+                    o[e + 4] = epi_t<ACT, false>(a1[e] + bias_s[f0 + 4 + e], (f16) 0);
+                }
+            }
+            *reinterpret_cast<f16x8 *>(crow + n) = o;
+        }
+    }
+}
+
 template <int BM, int BN, int STAGES, bool ROPE = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntiles) {
     constexpr int NW = 4, WN = 2;
@@ -1362,8 +1491,16 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     constexpr int LOADS = (BM + BN) / (8 * NW);    // wave-instructions per ring slice
     constexpr int NR = TM + TN, NM = TM * TN;      // fragment reads and MFMAs per k step
     static_assert(STAGES >= 2 && LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
+    static_assert(!ROPE || (BM == 128 && BN == 128), "the rope form is 128 x 128");
+    constexpr int EROW = BN + 4;                   // floats per staged row
+    constexpr int RING_BYTES = STAGES * (BM + BN) * DS_ROW * 2;
+    constexpr int STAGE_BYTES = 64 * EROW * 4;
+    constexpr int SLAB_BYTES = ROPE ? 2 * BIG_RD * BIG_SLAB_ROW * 4 : 0;
+    constexpr int BIAS_BYTES = ROPE ? BN * 4 : 0;
+    constexpr int EPI_BYTES = STAGE_BYTES + SLAB_BYTES + BIAS_BYTES;
+    constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
     // one buffer: the A ring, then the B ring; the epilogue reuses all of it
-    __shared__ __attribute__((aligned(16))) f16 lds[STAGES * (BM + BN) * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 lds[LDS_BYTES / 2];
     auto sA = [&](int st) { return lds + st * (BM * DS_ROW); };
     auto sB = [&](int st) { return lds + STAGES * (BM * DS_ROW) + st * (BN * DS_ROW); };
 
@@ -1378,25 +1515,21 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     const int KT = p.K / BK;
 
     // The epilogue's column chunk and bias (see below), loaded before the K loop.
-    constexpr int EROW = BN + 4;                   // floats per staged row
     constexpr int CPR = BN / 8, RPI = TPB / CPR;  // chunks per row, rows per sweep
-    static_assert(2 * 32 * EROW * 4 <= STAGES * (BM + BN) * DS_ROW * 2, "a staged row pair fits the ring");
     float *stage = reinterpret_cast<float *>(lds);
     const int tid = threadIdx.x, c8 = (tid % CPR) * 8, sr0 = tid / CPR, n = n0 + c8;
     const bool cols = tid < RPI * CPR && n < p.N;
-    // Rope (the rope entry point's guarantees plus rope_d % 8 == 0 and no
-    // residual): a chunk of 8 computed columns lies in one rope head or wholly
-    // past them, and holds two pair-interleaved quads (see rope_store4).
-    const bool rope = ROPE && cols && n < p.rope_cols;
-    const RopeQuad q0 = rope ? rope_quad(n, p.rope_d) : RopeQuad{}, q1 = rope ? rope_quad(n + 4, p.rope_d) : RopeQuad{};
-    // bias by computed column: a rope quad's columns are features lo, hi, lo + 1, hi + 1
     f32x4 b0 = {}, b1 = {};
-    if (p.bias && rope) {
-        b0 = f32x4{p.bias[q0.lo], p.bias[q0.hi], p.bias[q0.lo + 1], p.bias[q0.hi + 1]};
-        b1 = f32x4{p.bias[q1.lo], p.bias[q1.hi], p.bias[q1.lo + 1], p.bias[q1.hi + 1]};
-    } else if (p.bias && cols) {
+    if (!ROPE && p.bias && cols) {
         b0 = *reinterpret_cast<const f32x4 *>(p.bias + n);
         b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
+    }
+    // the rope form's tables and bias, loaded now (see big_rope_tables)
+    f32x4 tv[ROPE ? TM : 1][2][4];
+    float bias_own = 0.0f;
+    if constexpr (ROPE) {
+        big_rope_tables<BM, TM>(p, m0, tv);
+        bias_own = (tid < BN && p.bias && n0 + tid < p.N) ? p.bias[n0 + tid] : 0.0f;
     }
     f32x16 acc[TN][TM];
 #pragma unroll
@@ -1475,6 +1608,15 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     // ldc % 8 == 0 and 16-byte aligned C, R and bias.
     HX_WAIT_VMCNT(0);
     f16 *C = p.C;
+    if constexpr (ROPE) {
+        // the activation fixed at compile time: a runtime switch per output
+        // would split the unrolled epilogue into a branch per element
+        dispatch_epi(p.act, false, [&](auto act_c, auto) {
+            big_rope_epilogue<decltype(act_c)::value, BM, BN, TM, TN, EROW>(p, acc, stage, m0, n0, wave, lane, tv,
+                                                                            bias_own);
+        });
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         __builtin_amdgcn_s_barrier();              // the ring's (or the last pass's) reads are done
@@ -1490,53 +1632,6 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         if (!cols) continue;
         // staged rows 0..31 are block i of wave row 0, 32..63 of wave row 1
         auto row_of = [&](int sr) { return m0 + (sr >> 5) * (BM / 2) + i * 32 + (sr & 31); };
-        if constexpr (ROPE) {
-            if (rope) {
-                // the two quads' tables for row m: quad 0 uses table rows t0, t0 + 1 and
-                // their partners half further; quad 1 the next two
-                const int half = p.rope_d >> 1;
-                const long long ld = p.M;
-                struct Tab {
-                    float c[8], s[8];
-                };
-                auto tabs = [&](int sr) {
-                    Tab t{};
-                    const int m = row_of(sr);
-                    if (sr < 64 && m < p.M) {
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const long long o = (long long) (q0.t + u) * ld + m, oh = o + half * ld;
-                            t.c[u] = p.rcos[o];
-                            t.c[4 + u] = p.rcos[oh];
-                            t.s[u] = p.rsin[o];
-                            t.s[4 + u] = p.rsin[oh];
-                        }
-                    }
-                    return t;
-                };
-                Tab tn = tabs(sr0);
-                for (int sr = sr0; sr < 64; sr += RPI) {
-                    const Tab t = tn;
-                    tn = tabs(sr + RPI);
-                    const int m = row_of(sr);
-                    if (m >= p.M) continue;
-                    const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
-                    const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
-                    float x0[4], x1[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        x0[e] = f32_rounded(apply_act(v0[e] + b0[e], p.act));
-                        x1[e] = f32_rounded(apply_act(v1[e] + b1[e], p.act));
-                    }
-                    f16 *crow = C + (long long) m * p.ldc;
-                    rope_store4(crow, q0, x0, float2{t.c[0], t.c[1]}, float2{t.c[4], t.c[5]},
-                                float2{t.s[0], t.s[1]}, float2{t.s[4], t.s[5]});
-                    rope_store4(crow, q1, x1, float2{t.c[2], t.c[3]}, float2{t.c[6], t.c[7]},
-                                float2{t.s[2], t.s[3]}, float2{t.s[6], t.s[7]});
-                }
-                continue;
-            }
-        }
         auto resid = [&](int sr) {
             const int m = row_of(sr);
             return p.R && sr < 64 && m < p.M ? *reinterpret_cast<const f16x8 *>(p.R + (long long) m * p.ldr + n)
@@ -1765,39 +1860,6 @@ struct Tile {
     int bm, bn;
 };
 
-// Split-K workspace: grow-only per device, never freed while the process runs
-// (captured graphs may still reference an older buffer).
-struct Workspace {
-    std::mutex mu;
-    void *ptr[16] = {};
-    size_t size[16] = {};
-    size_t want[16] = {};
-};
-Workspace g_ws;
-
-int current_device() {
-    int d = 0;
-    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 16) d = 0;
-    return d;
-}
-
-// Workspace for `bytes`, or nullptr when it cannot be provided without an
-// allocation during stream capture (the caller then runs without split-K).
-float *workspace(size_t bytes) {
-    const int d = current_device();
-    std::lock_guard<std::mutex> g(g_ws.mu);
-    if (g_ws.size[d] >= bytes) return static_cast<float *>(g_ws.ptr[d]);
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(hx::stream(), &st) != hipSuccess || st != hipStreamCaptureStatusNone)
-        return nullptr;
-    void *p = nullptr;
-    const size_t sz = bytes < ((size_t) 64 << 20) ? ((size_t) 64 << 20) : bytes;
-    if (hipMalloc(&p, sz) != hipSuccess) return nullptr;
-    g_ws.ptr[d] = p;   // the previous buffer is intentionally kept alive
-    g_ws.size[d] = sz;
-    return static_cast<float *>(p);
-}
-
 // Chooses the tile and split count. Cost = (rounds of workgroups over the
 // 256 CUs x 2 resident workgroups each -- both tiles' kernels run at 2 waves
 // per SIMD) x (tile area / per-tile efficiency) x (K slices per split + a
@@ -1891,7 +1953,7 @@ bool launch_big(const GemmArgs &p, Tile t, int stages) {
     HX_BIG(256, 192, 2)
     HX_BIG(128, 256, 2)
     HX_BIG(128, 256, 3)
-    HX_BIG_ROPE(128, 192, 2)
+    HX_BIG(128, 192, 2)
     HX_BIG(128, 192, 3)
     HX_BIG(256, 128, 2)
     HX_BIG(256, 128, 3)
@@ -2011,12 +2073,15 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     const bool kw_ok = MODE == B_NK && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                        avec && bvec && (p.M + 31) / 32 <= 65535 && !p.ln_w;
     // the large-tile kernel: its epilogue stores 8-column chunks (and, with the
-    // rope, needs whole rope heads of 8-column chunks and no residual)
+    // rope, stages 64-wide heads' tables as 16-byte vectors of 4 rows: rope_d
+    // 64, M % 4 == 0, 16-byte aligned tables, whole 8-column chunks of rope
+    // columns, no residual)
     const bool big_ok = MODE == B_NK && batch == 1 && p.K % BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                         avec && bvec && !p.ln_w && p.N % 8 == 0 && p.ldc % 8 == 0 &&
                         ((uintptr_t) p.C & 15) == 0 && (!p.bias || ((uintptr_t) p.bias & 15) == 0) &&
                         (!p.R || (p.ldr % 8 == 0 && ((uintptr_t) p.R & 15) == 0)) &&
-                        (!p.rcos || (p.rope_d % 8 == 0 && p.rope_cols % 8 == 0 && !p.R));
+                        (!p.rcos || (p.rope_d == BIG_RD && p.rope_cols % 8 == 0 && !p.R && p.M % 4 == 0 &&
+                                     ((uintptr_t) p.rcos & 15) == 0 && ((uintptr_t) p.rsin & 15) == 0));
     if (big_ok && (path == 5 || path == 0)) {
         const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N);
         const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;
@@ -2107,8 +2172,8 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         const int per = (kt + splits - 1) / splits;
         splits = (kt + per - 1) / per;
         const size_t bytes = (size_t) batch * splits * (size_t) p.M * p.N * sizeof(float);
-        float *ws = hx::dry_run() ? nullptr : workspace(bytes);
-        if (hx::dry_run()) hx_reserve_workspace(bytes);
+        float *ws = hx::dry_run() ? nullptr : hx::workspace(bytes);
+        if (hx::dry_run()) hx::reserve_workspace(bytes);
         if (ws || hx::dry_run()) {
             p.splits = splits;
             p.k_per_split = per * BK;
@@ -2186,21 +2251,6 @@ GemmArgs args(const hexlib_hf *a, long long lda, long long sA, const void *b, lo
 }
 
 }  // namespace
-
-// Dry-run hook: the largest split-K workspace a validated blob will need, so
-// the session can allocate it before capturing a graph.
-static size_t g_reserve = 0;
-void hx_reserve_workspace(size_t bytes) {
-    if (bytes > g_reserve) g_reserve = bytes;
-}
-
-namespace hx {
-int prepare_workspace() {
-    const size_t want = g_reserve;
-    if (!want) return 0;
-    return workspace(want) ? 0 : -1;
-}
-}  // namespace hx
 
 extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
     const bool tile_ok = path == 5 ? (bm == 128 || bm == 256) && (bn == 128 || bn == 192 || bn == 256)

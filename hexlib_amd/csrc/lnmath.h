@@ -33,10 +33,12 @@ __device__ __forceinline__ void ln_row_stats(float (&v)[NCH][VEC], const bool (&
     inv = 1.0f / sqrtf(wave_sum(q) / (float) C + eps);
 }
 
-// One output element from its centred value d = x - mean, as an fp32 value
-// (f32_rounded: the caller's fp16 conversion then rounds it a second time, as
-// a stored fp32 result would be, never the exact fma in one step).
+// One output element from its centred value d = x - mean, as an fp32 value:
+// ((d * inv) * w) + b with each product and the sum rounded to fp32 as
+// written (kernels/layernorm_fp16/baseline.c:33 rounds three times; contraction
+// is off, so no fused multiply-add). f32_rounded keeps the caller's fp16
+// conversion a second, separate rounding of that fp32 result.
 __device__ __forceinline__ float ln_apply(float d, float inv, float w, float b) {
 #pragma clang fp contract(off)
-    return f32_rounded(__builtin_fmaf(d * inv, w, b));
+    return f32_rounded(d * inv * w + b);
 }

@@ -26,29 +26,96 @@
 
 namespace hx {
 
-static std::atomic<hipStream_t> g_stream{nullptr};
-static std::atomic<int> g_error{0};
+// Per host thread: two threads (say, two sessions invoked concurrently) never
+// launch on each other's stream or take each other's launch errors.
+static thread_local hipStream_t t_stream = nullptr;
+static thread_local int t_error = 0;
 static thread_local bool t_dry_run = false;
 
-hipStream_t stream() { return g_stream.load(std::memory_order_relaxed); }
+hipStream_t stream() { return t_stream; }
 
 void note(hipError_t e) {
-    if (e != hipSuccess) {
-        int expected = 0;
-        g_error.compare_exchange_strong(expected, (int) e);
-    }
+    if (e != hipSuccess && t_error == 0) t_error = (int) e;
 }
 
 bool dry_run() { return t_dry_run; }
 void set_dry_run(bool on) { t_dry_run = on; }
 
+// ---- scratch ----
+
+constexpr int MAX_DEVICES = 16;
+
+struct Scratch {
+    std::mutex mu;
+    void *ptr[MAX_DEVICES] = {};
+    size_t size[MAX_DEVICES] = {};
+    // buffers replaced by a larger one: a graph captured earlier may still
+    // read them, so they live until the scratch is freed
+    std::vector<void *> retired;
+};
+
+static Scratch g_default_scratch;
+static thread_local Scratch *t_scratch = nullptr;
+static thread_local size_t t_reserve = 0;
+
+Scratch *scratch_new() { return new (std::nothrow) Scratch(); }
+
+void scratch_free(Scratch *s) {
+    if (!s) return;
+    for (int d = 0; d < MAX_DEVICES; ++d)
+        if (s->ptr[d]) hipFree(s->ptr[d]);
+    for (void *p : s->retired) hipFree(p);
+    delete s;
+}
+
+Scratch *current_scratch() { return t_scratch ? t_scratch : &g_default_scratch; }
+void set_current_scratch(Scratch *s) { t_scratch = s; }
+
+static int current_device() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= MAX_DEVICES) d = 0;
+    return d;
+}
+
+float *workspace(size_t bytes) {
+    Scratch *s = current_scratch();
+    const int d = current_device();
+    std::lock_guard<std::mutex> g(s->mu);
+    if (s->size[d] >= bytes) return static_cast<float *>(s->ptr[d]);
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream(), &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+        return nullptr;
+    void *p = nullptr;
+    const size_t sz = bytes < ((size_t) 64 << 20) ? ((size_t) 64 << 20) : bytes;
+    if (hipMalloc(&p, sz) != hipSuccess) return nullptr;
+    if (s->ptr[d]) s->retired.push_back(s->ptr[d]);
+    s->ptr[d] = p;
+    s->size[d] = sz;
+    return static_cast<float *>(p);
+}
+
+void reserve_workspace(size_t bytes) {
+    if (bytes > t_reserve) t_reserve = bytes;
+}
+
+int prepare_workspace() {
+    const size_t want = t_reserve;
+    t_reserve = 0;
+    if (!want) return 0;
+    return workspace(want) ? 0 : -1;
+}
+
 }  // namespace hx
 
 extern "C" {
 
-void hexlib_gpu_set_stream(void *stream) { hx::g_stream.store((hipStream_t) stream); }
-void *hexlib_gpu_get_stream(void) { return (void *) hx::g_stream.load(); }
-int hexlib_gpu_take_error(void) { return hx::g_error.exchange(0); }
+void hexlib_gpu_set_stream(void *stream) { hx::t_stream = (hipStream_t) stream; }
+void *hexlib_gpu_get_stream(void) { return (void *) hx::t_stream; }
+int hexlib_gpu_take_error(void) {
+    const int e = hx::t_error;
+    hx::t_error = 0;
+    return e;
+}
 const char *hexlib_gpu_error_string(int e) { return hipGetErrorString((hipError_t) e); }
 
 const char *hexlib_gpu_status_name(int s) {
@@ -118,6 +185,9 @@ struct hexlib_gpu_ctx {
     uint32_t graph_nops = 0;
 
     std::vector<hipEvent_t> events;
+
+    // this session's split-K workspace (never shared with another session)
+    hx::Scratch *scratch = nullptr;
 };
 
 namespace {
@@ -142,16 +212,21 @@ hexlib_gpu_ctx::Slot *find_fd(hexlib_gpu_ctx *ctx, uint32_t fd) {
     return nullptr;
 }
 
-uint64_t elem_capacity_ok(const hexlib_tensor &t) {
-    // 1 if ne fits nbytes for the declared dtype, else 0.
-    const uint64_t n = (uint64_t) t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+bool elem_capacity_ok(const hexlib_tensor &t) {
+    // True if ne fits nbytes for the declared dtype. The element count is a
+    // product of four uint32 factors, each widened before its multiply (the
+    // product stays below 2^128); it is compared against nbytes divided by the
+    // element size, so no side of the comparison can wrap.
+    typedef unsigned __int128 u128;
+    const u128 n = (u128) t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    const u128 nb = t.nbytes;
     switch (t.dtype) {
     case HEXLIB_DTYPE_FP32:
-    case HEXLIB_DTYPE_INT32: return n * 4 <= t.nbytes;
-    case HEXLIB_DTYPE_FP16: return n * 2 <= t.nbytes;
-    case HEXLIB_DTYPE_Q4_0: return n % 32 == 0 && n / 32 * 18 <= t.nbytes;
-    case HEXLIB_DTYPE_Q8_0: return n % 32 == 0 && n / 32 * 34 <= t.nbytes;
-    default: return 0;
+    case HEXLIB_DTYPE_INT32: return n <= nb / 4;
+    case HEXLIB_DTYPE_FP16: return n <= nb / 2;
+    case HEXLIB_DTYPE_Q4_0: return n % 32 == 0 && n / 32 <= nb / 18;
+    case HEXLIB_DTYPE_Q8_0: return n % 32 == 0 && n / 32 <= nb / 34;
+    default: return false;
     }
 }
 
@@ -289,6 +364,12 @@ struct StreamScope {
     ~StreamScope() { hexlib_gpu_set_stream(saved); }
 };
 
+struct ScratchScope {
+    hx::Scratch *saved;
+    explicit ScratchScope(hx::Scratch *s) : saved(hx::current_scratch()) { hx::set_current_scratch(s); }
+    ~ScratchScope() { hx::set_current_scratch(saved); }
+};
+
 struct DryScope {
     bool saved;
     explicit DryScope(bool on) : saved(hx::dry_run()) { hx::set_dry_run(on); }
@@ -303,6 +384,11 @@ int hexlib_gpu_open(hexlib_gpu_ctx **out) {
     if (!out) return HEXLIB_DSP_ERR_INVAL_PARAMS;
     hexlib_gpu_ctx *ctx = new (std::nothrow) hexlib_gpu_ctx();
     if (!ctx) return HEXLIB_DSP_ERR_INTERNAL;
+    ctx->scratch = hx::scratch_new();
+    if (!ctx->scratch) {
+        delete ctx;
+        return HEXLIB_DSP_ERR_INTERNAL;
+    }
     for (auto &m : ctx->mmap) {
         m.base = nullptr;
         m.size = 0;
@@ -342,7 +428,8 @@ int hexlib_gpu_stop(hexlib_gpu_ctx *ctx) {
 
 int hexlib_gpu_close(hexlib_gpu_ctx *ctx) {
     if (!ctx) return HEXLIB_DSP_ERR_INVAL_PARAMS;
-    hexlib_gpu_stop(ctx);
+    hexlib_gpu_stop(ctx);   // drains the session stream first
+    hx::scratch_free(ctx->scratch);
     delete ctx;
     return HEXLIB_DSP_OK;
 }
@@ -421,6 +508,7 @@ int hexlib_gpu_invoke(hexlib_gpu_ctx *ctx, const uint8_t *batch, uint32_t len, u
         return rc;
     }
 
+    ScratchScope scratch_scope(ctx->scratch);
     auto *results = reinterpret_cast<hexlib_op_result *>(rsp + sizeof(hexlib_batch_rsp_hdr));
     uint32_t done = 0;
     uint64_t total_ns = 0;

@@ -23,6 +23,7 @@ is current.
 from __future__ import annotations
 
 import os
+import re
 import sys
 
 from hexlib_amd.exec.runner import KIND_ID, SPECS, WIRE_RAW, RunnerSpec
@@ -31,6 +32,40 @@ from hexlib_amd.exec.wire import DTYPE_ID, LAYOUT_ID
 _CTYPE = {"fp16": "hexlib_hf", "fp32": "float", "int32": "int"}
 OUT_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
                         "csrc", "gen_entries.cpp")
+
+
+_NAME = re.compile(r"[A-Za-z_][A-Za-z0-9_]*|[0-9]+")
+
+
+def _top_level_factors(ext: str) -> list[str]:
+    out, depth, cur = [], 0, ""
+    for ch in ext:
+        depth += ch == "("
+        depth -= ch == ")"
+        if ch == "*" and depth == 0:
+            out.append(cur.strip())
+            cur = ""
+        else:
+            cur += ch
+    out.append(cur.strip())
+    return out
+
+
+def _wide(ext: str) -> str:
+    """An extent (a product of scalars, literals and parenthesised
+    multiply-free int expressions, optionally written with a leading
+    `(uint64_t)` cast) as a saturating 128-bit product: each factor is widened
+    before it is multiplied and a product that would pass 2^128 saturates, so
+    the comparison against a buffer's element count can never wrap."""
+    factors = _top_level_factors(ext.replace("(uint64_t)", ""))
+    for f in factors:
+        if not (_NAME.fullmatch(f) or (f.startswith("(") and f.endswith(")") and "*" not in f)):
+            raise ValueError(f"extent {ext!r}: factor {f!r} is not a name, a literal or a "
+                             f"multiply-free parenthesised expression")
+    expr = f"(hx_u128) {factors[0]}"
+    for f in factors[1:]:
+        expr = f"hx_mul_sat({expr}, (hx_u128) {f})"
+    return expr
 
 
 def _scalar_expr(src: str, ctype: str, param_index: int) -> str:
@@ -83,13 +118,13 @@ def emit_entry(name: str, spec: RunnerSpec) -> str:
                     lines.append(f"    if ({sc.name} <= 0) return HEXLIB_DSP_ERR_INVAL_PARAMS;")
         else:
             expr = _scalar_expr(sc.source, sc.ctype, param_index)
-            lines.append(f"    const uint64_t {sc.name}_u = {expr};")
+            lines.append(f"    const hx_u128 {sc.name}_u = {expr};")
             lines.append(f"    if ({sc.name}_u == 0 || {sc.name}_u > 0x7fffffffu) "
                          f"return HEXLIB_DSP_ERR_INVAL_PARAMS;")
             lines.append(f"    const int {sc.name} = (int) {sc.name}_u;")
         args_scalar.append(sc.name)
     for i, ext in enumerate(spec.extents):
-        lines.append(f"    if ((unsigned __int128) ({ext}) > (unsigned __int128) hx_numel(a, {i})) "
+        lines.append(f"    if ({_wide(ext)} > hx_numel(a, {i})) "
                      f"return HEXLIB_DSP_ERR_INVAL_PARAMS;")
     for cond in spec.checks:
         lines.append(f"    if (!({cond})) return HEXLIB_DSP_ERR_INVAL_PARAMS;")
@@ -115,8 +150,16 @@ def generate() -> str:
         '#include "internal.h"',
         '',
         'namespace {',
-        'inline uint64_t hx_numel(const hexlib_args *a, int i) {',
-        '    return (uint64_t) a->ne[i][0] * a->ne[i][1] * a->ne[i][2] * a->ne[i][3];',
+        'typedef unsigned __int128 hx_u128;',
+        '// Element count of buffer i: four uint32 factors, widened before each',
+        '// multiply, so the product (< 2^128) never wraps.',
+        'inline hx_u128 hx_numel(const hexlib_args *a, int i) {',
+        '    return (hx_u128) a->ne[i][0] * a->ne[i][1] * a->ne[i][2] * a->ne[i][3];',
+        '}',
+        '// a * b, or the largest value where the product would pass 2^128.',
+        'inline hx_u128 hx_mul_sat(hx_u128 a, hx_u128 b) {',
+        '    hx_u128 r;',
+        '    return __builtin_mul_overflow(a, b, &r) ? ~(hx_u128) 0 : r;',
         '}',
         '// A launch error recorded while running an entry is an op failure.',
         'inline int hx_entry_status() {',

@@ -138,40 +138,63 @@ class Graph:
             raise KeyError(f"no tensor named {name!r} in this graph") from None
 
     def problems(self) -> list[str]:
-        """Structural defects as readable strings; empty means valid
-        (reference `ir.py:175-225`). An empty graph is itself a defect."""
-        out: list[str] = []
-        if not self.ops:
-            out.append("graph has no ops")
-        if not self.outputs:
-            out.append("graph declares no outputs")
-        for key, t in self.tensors.items():
+        """Structural defects as readable strings; empty means valid. Covers
+        what the reference validator rejects (`ir.py:175-225`): a graph must
+        have ops and outputs, ids must be unique, every name an op or the graph
+        touches must be declared, a tensor has exactly one producer (a graph
+        input or const counts as one) and every read comes after it.
+
+        Built as two passes: the first records, for every tensor, where its
+        value comes from (a source or the position of its producing op) and
+        flags second producers; the second checks each read against that
+        table, so a read before its producer and a read of a tensor nobody
+        produces are told apart."""
+        bad: list[str] = []
+        declared = self.tensors
+        for key, t in declared.items():
             if key != t.name:
-                out.append(f"tensor keyed {key!r} is named {t.name!r}")
-        written = set(self.inputs) | {t.name for t in self.tensors.values() if t.const}
-        ids: set[int] = set()
-        for op in self.ops:
-            if op.id in ids:
-                out.append(f"duplicate op id {op.id}")
-            ids.add(op.id)
-            for name in op.inputs:
-                if name not in self.tensors:
-                    out.append(f"op {op.id} ({op.kind}) reads undeclared tensor {name!r}")
-                elif name not in written:
-                    out.append(f"op {op.id} ({op.kind}) reads {name!r} before it is written")
-            for name in op.outputs:
-                if name not in self.tensors:
-                    out.append(f"op {op.id} ({op.kind}) writes undeclared tensor {name!r}")
-                elif name in written:
-                    out.append(f"tensor {name!r} is written twice (op {op.id})")
-                else:
-                    written.add(name)
+                bad.append(f"tensors[{key!r}] holds a tensor called {t.name!r}")
+        if not self.ops:
+            bad.append("empty graph: no ops to run")
+        if not self.outputs:
+            bad.append("empty graph: nothing marked as an output")
+
+        SOURCE = -1
+        origin: dict[str, int] = {}
         for name in self.inputs:
-            if name not in self.tensors:
-                out.append(f"graph input {name!r} is not declared")
+            if name not in declared:
+                bad.append(f"input {name!r}: not in the tensor table")
+            origin[name] = SOURCE
+        for t in declared.values():
+            if t.const:
+                origin.setdefault(t.name, SOURCE)
+        seen_ids: dict[int, int] = {}
+        for pos, op in enumerate(self.ops):
+            if op.id in seen_ids:
+                bad.append(f"ops[{pos}] and ops[{seen_ids[op.id]}] share id {op.id}")
+            seen_ids.setdefault(op.id, pos)
+            for name in op.outputs:
+                if name not in declared:
+                    bad.append(f"{op.kind} #{op.id}: output {name!r} not in the tensor table")
+                elif name in origin:
+                    first = "a graph input or const" if origin[name] == SOURCE else \
+                        f"{self.ops[origin[name]].kind} #{self.ops[origin[name]].id}"
+                    bad.append(f"{op.kind} #{op.id}: output {name!r} already produced by {first}")
+                else:
+                    origin[name] = pos
+
+        for pos, op in enumerate(self.ops):
+            for name in op.inputs:
+                if name not in declared:
+                    bad.append(f"{op.kind} #{op.id}: input {name!r} not in the tensor table")
+                elif name not in origin:
+                    bad.append(f"{op.kind} #{op.id}: input {name!r} has no producer")
+                elif origin[name] >= pos:
+                    bad.append(f"{op.kind} #{op.id}: input {name!r} is produced later, by op "
+                               f"#{self.ops[origin[name]].id}")
         for name in self.outputs:
-            if name not in self.tensors:
-                out.append(f"graph output {name!r} is not declared")
-            elif name not in written:
-                out.append(f"graph output {name!r} is never written")
-        return out
+            if name not in declared:
+                bad.append(f"output {name!r}: not in the tensor table")
+            elif name not in origin:
+                bad.append(f"output {name!r}: no op produces it")
+        return bad

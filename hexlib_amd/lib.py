@@ -47,6 +47,7 @@ SIGNATURES = {
     "attention_qk_v_fp16": (None, [_P, _P, _P, _I, _I, _I, _I, _F]),
     "rope_2d_qk_fp16": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "hexlib_gpu_gemm_override": (_I, [_I, _I, _I, _I]),
+    "hexlib_gpu_attention_override": (_I, [_I]),
     "hexlib_gpu_set_stream": (None, [_P]),
     "hexlib_gpu_get_stream": (_P, []),
     "hexlib_gpu_take_error": (_I, []),

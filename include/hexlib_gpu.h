@@ -318,6 +318,14 @@ const char *hexlib_gpu_status_name(int status);
  * back to the automatic choice); 2 to 5 apply where their preconditions
  * hold). Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
 int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path);
+/* Tuning override (no reference counterpart) for the attention kernels'
+ * form, for every later attention launch in the process: 0 = automatic,
+ * 1 = the per-wave-tiles kernel (32 queries per workgroup, waves split the
+ * keys), QG * 10 + KS = the shared-K/V kernel with QG 32-query groups and KS
+ * key splits (41, 21, 22, 42; a form not built for the head width falls
+ * back to the per-wave-tiles kernel). Returns HEXLIB_DSP_OK or
+ * ERR_INVAL_PARAMS. */
+int hexlib_gpu_attention_override(int form);
 /* sizeof of each wire struct, in declaration order above (batch_hdr, buf_desc,
  * tensor, op_desc, rsp_hdr, op_result, hexlib_args); returns the count. */
 uint32_t hexlib_gpu_struct_sizes(uint32_t *out, uint32_t cap);

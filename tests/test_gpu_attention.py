@@ -108,7 +108,8 @@ def test_rope_2d_qk_and_attention_qk_v(dev, B, T, H, D):
     assert K.close_f16(got, want, 1e-2, 1e-3).all()
 
 
-@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (2, 33, 2, 64), (3, 17, 2, 32)])
+@pytest.mark.parametrize("B,T,H,D", [(1, 256, 12, 64), (1, 784, 12, 64), (2, 33, 2, 64), (3, 17, 2, 32),
+                                     (32, 256, 12, 64)])
 def test_attention_qkv(dev, B, T, H, D):
     """KIND 23: q, k, v all read from one [rows, 3, H, D] tensor -- the output
     of the q/k/v linear with rope in its epilogue. Bit-identical to KIND 19 fed
@@ -128,3 +129,30 @@ def test_attention_qkv(dev, B, T, H, D):
     want = K.attention_fp16(qkv[:, 0], qkv[:, 1], qkv[:, 2], B, D ** -0.5)
     report(f"attention_qkv B{B} T{T} H{H} D{D}", got, want)
     assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+@pytest.mark.parametrize("form", [41, 21, 22, 42, 1])
+@pytest.mark.parametrize("B,T,H,D", [(4, 256, 2, 64), (1, 784, 2, 64), (2, 100, 3, 64), (3, 33, 2, 32),
+                                     (1, 1, 1, 64), (2, 130, 2, 32)])
+def test_attention_forms(dev, form, B, T, H, D):
+    """Every attention form, forced through the override: the shared-K/V
+    kernel with QG query groups and KS key splits (form QG * 10 + KS; the
+    D = 32 build has 41 and 22, other forms fall back), and the per-wave-tiles
+    kernel (1). Ragged T leaves partial query groups, partial 64-key stages
+    and key splits with no stage at all; each against the float64 oracle."""
+    r = np.random.default_rng(100 + T + form)
+    q, k, v = (h16(r.standard_normal((B * T, H, D))) for _ in range(3))
+    assert dev.lib.hexlib_gpu_attention_override(form) == 1
+    try:
+        got = run(dev, q, k, v, B, D ** -0.5)
+    finally:
+        dev.lib.hexlib_gpu_attention_override(0)
+    want = K.attention_fp16(q, k, v, B, D ** -0.5)
+    report(f"attention form {form} B{B} T{T} H{H} D{D}", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+
+
+def test_attention_override_rejects_unknown_forms(dev):
+    for form in (2, 3, 11, 14, 44, -1):
+        assert dev.lib.hexlib_gpu_attention_override(form) != 1
+    assert dev.lib.hexlib_gpu_attention_override(0) == 1

@@ -573,12 +573,16 @@ def test_big_tile_path(dev, form, M, Kd, N, act, resid):
 
 @pytest.mark.parametrize("form", [(128, 128, 2), (128, 192, 2), None])
 @pytest.mark.parametrize("M,Kd,heads,d,extra,act", [(1100, 768, 12, 64, 768, 0), (300, 256, 3, 16, 64, 1),
-                                                    (520, 512, 4, 32, 128, 2), (2048, 768, 12, 64, 768, 0)])
+                                                    (520, 512, 4, 32, 128, 2), (2048, 768, 12, 64, 768, 0),
+                                                    (1102, 768, 4, 64, 128, 1), (2048, 256, 2, 64, 0, 2)])
 def test_big_tile_rope_epilogue(dev, form, M, Kd, heads, d, extra, act):
     """The large-tile kernel's rope epilogue (forced with path 5, or the
     automatic choice where the grid fills a round: form None) is bit-identical
     to the same kernel's plain output followed by rope_2d on the q and k
-    heads; ragged M, head widths 16 to 64, every activation."""
+    heads; ragged M, head widths 16 to 64, every activation. Its 128 x 128
+    form stages each pass's tables in LDS (rope_d 64, M % 4 == 0); the other
+    cases (M = 1102, narrower heads, the 128 x 192 tile) take the other rope
+    epilogues."""
     r = rng(23)
     N = 2 * heads * d + extra
     a = h16(r.standard_normal((M, Kd)))
@@ -784,3 +788,66 @@ def test_q4k_kw_path(dev, tile, M, Kd, N, act):
     np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
     assert K.close_f16(got, dev.down(d3), 0.01, 3e-4).all()
     assert K.close_f16(got, K.matmul_q4k(a, wq, bias, Kd, N, act), 0.01, 3e-4).all()
+
+
+# ---- the reference harnesses' adversarial cells --------------------------------------
+
+def test_matmul_harness_adversarial_element(dev):
+    """`kernels/matmul_fp16/harness.c`'s shape (3, 40, 128, 200) and its
+    element C[1][5][7]: one dominant product plus 127 one-ulp followers. The
+    kernel is within the matmul bound of the oracle there (2.1240234375 in
+    fp32, one rounding); the fp16-accumulating near-miss (2.0) is not, so this
+    test would reject a kernel that carried it."""
+    from tests import harness_data as HD, nearmiss as NM
+    A, B, (b, m, n) = HD.matmul_adversarial()
+    dA, dB, dC = dev.up(A), dev.up(B), dev.empty((3, 40, 200), np.float16)
+    dev.lib.matmul_fp16(dev.ptr(dA), dev.ptr(dB), dev.ptr(dC), 3, 40, 128, 200)
+    dev.check()
+    got, want = dev.down(dC), K.matmul_fp16(A, B)
+    report("matmul harness", got, want)
+    assert K.close_f16(got, want, 1e-2, 1e-3).all()
+    assert abs(float(got[b, m, n]) - 2.1240234375) <= 1e-3
+    assert not K.close_f16(got, NM.matmul_fp16_accumulate(A, B), 1e-2, 1e-3).all()
+
+
+def test_epilogue_harness_cell1(dev):
+    """`kernels/matmul_epilogue_fp16/harness.c` cell 1 on the reference-ABI
+    q4_0 GEMM: out[0, 0] = 1 + 63 * 2^-12 (1.015625 once rounded); the
+    fp16-running-sum near-miss gives 1.0 and fails the epilogue bound."""
+    from tests import harness_data as HD, nearmiss as NM
+    a, w, bias, M, Kd, N, act = HD.epilogue_cell1()
+    da, db = dev.up(a), dev.up(bias)
+    dw = dev.up(np.frombuffer(w, np.uint8))
+    dout = dev.empty((M, N), np.float16)
+    dev.lib.matmul_epilogue_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dout), M, Kd, N, act)
+    dev.check()
+    got = dev.down(dout)
+    assert K.close_f16(got, K.matmul_epilogue_fp16(a, w, bias, Kd, N, act), 0.01, 3e-4).all()
+    assert float(got[0, 0]) == 1.015625
+    bad = NM.epilogue_fp16_accumulation(a, NM.dense_q4_nblocked(w, Kd, N), bias, act)
+    assert not K.close_f16(got, bad, 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("path", [0, 1, 2, 3, 4])
+def test_f16wt_harness_cell1_every_path(dev, path):
+    """Cell 1 on the fp16-weight W^T linear at K = 768, through every small-M
+    code path (automatic, register-staged, direct-to-LDS, small-M register
+    operands, K across waves): each within the epilogue bound of the oracle,
+    and none as close to the fp16-running-sum near-miss (1.0 at [0, 0], where
+    the value is 1.1872...)."""
+    from tests import harness_data as HD, nearmiss as NM
+    a, w, bias, act = HD.epilogue_cell1_f16()
+    M, Kd = a.shape
+    N = w.shape[1]
+    da, dw, db = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias)
+    dout = dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, path) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dout), M, Kd, N, act)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    got = dev.down(dout)
+    assert K.close_f16(got, K.matmul_epilogue_f16w(a, w, bias, act), 0.01, 3e-4).all()
+    assert abs(float(got[0, 0]) - 1.1872558) < 1e-3
+    assert not K.close_f16(got, NM.epilogue_fp16_accumulation(a, w, bias, act), 0.01, 3e-4).all()

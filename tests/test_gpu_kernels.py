@@ -187,3 +187,52 @@ def test_invalid_dims_are_silent_no_ops(dev):
     dev.lib.patchify_fp32(dev.ptr(dx), dev.ptr(dy), 3, 1, 10, 10, 3, 2, 4, 4)   # 4*3 != 10
     dev.check()
     assert (dev.down(dy) == np.float16(12345.0)).all()
+
+
+# ---- the reference harnesses' adversarial rows ----------------------------------------
+
+def test_softmax_harness_rows(dev):
+    """`kernels/softmax_fp16/harness.c` rows 0 (a 90.0: exp overflows without
+    the max subtracted) and 1 (one 20.0 and 255 followers at 13.5: an fp16
+    running sum loses 8% of the denominator): within (0.01, 1e-3) of the
+    oracle, and the two near-misses are not."""
+    from tests import harness_data as HD, nearmiss as NM
+    x = HD.softmax_rows()
+    dx, dy = dev.up(x), dev.empty(x.shape, np.float16)
+    dev.lib.softmax_fp16(dev.ptr(dx), dev.ptr(dy), 6, 256)
+    dev.check()
+    got = dev.down(dy)
+    assert K.close_f16(got, K.softmax_fp16(x), 0.01, 1e-3).all()
+    assert not K.close_f16(got[1:2], NM.softmax_sum_fp16(x)[1:2], 0.01, 1e-3).all()
+    with np.errstate(invalid="ignore"):
+        assert not K.close_f16(got, NM.softmax_no_max_subtraction(x), 0.01, 1e-3).all()
+
+
+def test_rmsnorm_harness_eps_row(dev):
+    """`kernels/rmsnorm_fp16/harness.c` row 0 (values of 1e-4, where eps
+    dominates the mean square): within (0.02, 1e-3), and the no-eps
+    near-miss is not."""
+    from tests import harness_data as HD, nearmiss as NM
+    x, w, eps = HD.rmsnorm_rows()
+    dx, dw, dy = dev.up(x), dev.up(w), dev.empty(x.shape, np.float16)
+    dev.lib.rmsnorm_fp16(dev.ptr(dx), dev.ptr(dw), dev.ptr(dy), x.shape[0], x.shape[1], eps)
+    dev.check()
+    got = dev.down(dy)
+    assert K.close_f16(got, K.rmsnorm_fp16(x, w, eps), 0.02, 1e-3).all()
+    assert not K.close_f16(got[:1], NM.rmsnorm_no_eps(x, w, eps)[:1], 0.02, 1e-3).all()
+
+
+def test_rope_harness_near_cancellation(dev):
+    """`kernels/rope_2d_fp16/harness.c`'s crafted last token: two products of
+    about 500 that cancel to -0.1 and 0.1. Bit-exact with the oracle; the
+    fp16-products and table-by-head near-misses are outside (0.02, 1e-3)."""
+    from tests import harness_data as HD, nearmiss as NM
+    x, cos, sin = HD.rope_near_cancellation()
+    T, Hh, D = x.shape
+    dx, dc, ds, dy = dev.up(x), dev.up(cos), dev.up(sin), dev.empty(x.shape, np.float16)
+    dev.lib.rope_2d_fp16(dev.ptr(dx), dev.ptr(dc), dev.ptr(ds), dev.ptr(dy), T, Hh, D)
+    dev.check()
+    got = dev.down(dy)
+    exact(got, K.rope_2d_fp16(x, cos, sin))
+    assert not K.close_f16(got[-1:], NM.rope_fp16_products(x, cos, sin)[-1:], 0.02, 1e-3).all()
+    assert not K.close_f16(got, NM.rope_table_by_head(x, cos, sin), 0.02, 1e-3).all()

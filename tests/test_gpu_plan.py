@@ -274,3 +274,44 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     print(f"[{mode} residual={residual} rope={rope} ln={ln} {image} b{batch}] max abs vs reference graph "
           f"{err:.3e}", flush=True)
     assert err <= 2e-2
+
+
+def _image_feeds(cfg1, feeds_b, i):
+    """Image i's feeds at batch 1, sliced from a batch's feeds: its channels of
+    the stacked image, its rows of the per-token tables, every const shared."""
+    g1 = E.build_vision_encoder(cfg1)
+    n = cfg1.num_tokens
+    c = cfg1.in_channels
+    f1 = {}
+    for t in g1.tensors.values():
+        if t.name == "image":
+            f1["image"] = feeds_b["image"][i * c:(i + 1) * c]
+        elif t.name in ("pos_embed", "rope_cos", "rope_sin"):
+            f1[t.name] = feeds_b[t.name][i * n:(i + 1) * n]
+        elif t.const:
+            f1[t.name] = feeds_b[t.name]
+    return f1
+
+
+def test_product_plan_at_batch_32(session):
+    """BASELINE cfg 4 at batch 32 (M = 8192 for every linear), run as the
+    bench's product plan: fused attention over one q/k/v projection with the
+    q/k rope in its GEMM epilogue, residual adds in the proj/fc2 epilogues,
+    W^T weights. Images 0, 17 and 31 are each checked against the storage-
+    rounding oracle of the REFERENCE graph at batch 1 on that image's feeds
+    (the reference executor is single-image, `hexlib/exec/interpreter.py:80-205`);
+    the whole-encoder bar is 2e-2 max abs."""
+    cfg1 = E.QWEN35_VISION_FP16
+    cfg_ref = replace(cfg1, batch=32)
+    g_ref = E.build_vision_encoder(cfg_ref)
+    feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=6)
+    cfg = replace(cfg_ref, attention="fused_qkv_rope")
+    (out,), wb = _run_plan(session, cfg, E.fuse_qkv_feeds(feeds, cfg), graph_mode=True, residual=True,
+                           rope=True, weight_layout="auto")
+    assert wb.n_ops == 259 - 12 * 11 - 24 - 12
+    per = out.shape[0] // 32
+    for i in (0, 17, 31):
+        want = _oracle(cfg1, _image_feeds(cfg1, feeds, i))
+        err = np.abs(out[i * per:(i + 1) * per] - want).max()
+        print(f"[product plan b32] image {i}: max abs vs reference graph {err:.3e}", flush=True)
+        assert err <= 2e-2

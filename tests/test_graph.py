@@ -303,3 +303,36 @@ def test_fuse_layernorm():
     assert wb.n_ops == 259 - 12 * 11 - 24 - 12 - 12
     assert sum(1 for s in wb.op_specs if s == "layernorm_matmul_epilogue_f16wt") == 12
     assert KIND_ID_OF("layernorm_matmul_epilogue_f16wt") == 24
+
+
+def test_problems_names_every_structural_defect():
+    """Each defect the reference validator rejects (`hexlib/graph/ir.py:175-225`)
+    is reported, and a well-formed graph reports none."""
+    from hexlib_amd.graph.ir import Graph, Op, Tensor
+
+    def T(n, const=False):
+        return Tensor(n, "fp16", (4,), const)
+
+    ok = Graph({n: T(n) for n in "xyz"} | {"w": T("w", True)},
+               (Op(0, "add", ("x", "w"), ("y",)), Op(1, "scale", ("y",), ("z",))), ("x",), ("z",))
+    assert ok.problems() == []
+
+    def probs(ops, inputs=("x",), outputs=("z",), extra=()):
+        tens = {n: T(n) for n in "xyz"} | {"w": T("w", True)} | {t.name: t for t in extra}
+        return " | ".join(Graph(tens, tuple(ops), inputs, outputs).problems())
+
+    assert "no ops" in probs([], outputs=("x",))
+    assert "nothing marked as an output" in probs([Op(0, "scale", ("x",), ("z",))], outputs=())
+    assert "share id 0" in probs([Op(0, "scale", ("x",), ("y",)), Op(0, "scale", ("y",), ("z",))])
+    assert "input 'q' not in the tensor table" in probs([Op(0, "add", ("x", "q"), ("z",))])
+    assert "output 'q' not in the tensor table" in probs([Op(0, "scale", ("x",), ("q",)),
+                                                           Op(1, "scale", ("x",), ("z",))])
+    assert "input 'y' has no producer" in probs([Op(0, "add", ("x", "y"), ("z",))])
+    assert "produced later" in probs([Op(0, "scale", ("y",), ("z",)), Op(1, "scale", ("x",), ("y",))])
+    assert "already produced by scale #0" in probs([Op(0, "scale", ("x",), ("z",)),
+                                                    Op(1, "scale", ("x",), ("z",))])
+    assert "already produced by a graph input" in probs([Op(0, "scale", ("w",), ("x",)),
+                                                         Op(1, "scale", ("x",), ("z",))])
+    assert "output 'z': no op produces it" in probs([Op(0, "scale", ("x",), ("y",))])
+    assert "input 'q': not in the tensor table" in probs([Op(0, "scale", ("x",), ("z",))],
+                                                          inputs=("x", "q"))

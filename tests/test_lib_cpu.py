@@ -189,6 +189,39 @@ def test_extent_larger_than_nbytes_is_refused(sess):
     assert sess.invoke(blob)[0] == wire.STATUS["ERR_INVAL_PARAMS"]
 
 
+@pytest.mark.parametrize("ne,want", [
+    ((2, 4, 8, 1), "OK"),                                  # 64 elements in 128 bytes
+    ((2, 8, 8, 1), "ERR_INVAL_PARAMS"),                    # an honest oversize
+    ((1 << 15, 1 << 19, 1 << 30, 1), "ERR_INVAL_PARAMS"),  # B*T*D = 2^64: wraps to 0 in 64 bits
+    ((1 << 16, 1 << 16, 1 << 16, 1 << 16), "ERR_INVAL_PARAMS"),  # numel 2^64 with a fourth axis
+    # 64 * (2^29 + 2^15 + 1) * (2^29 - 2^15 + 1) = 2^64 + 64: wraps to exactly 64
+    ((64, (1 << 29) + (1 << 15) + 1, (1 << 29) - (1 << 15) + 1, 1), "ERR_INVAL_PARAMS"),
+])
+def test_extents_that_wrap_64_bits_are_refused(sess, ne, want):
+    """Both sides of every capacity check (the extent the kernel will touch
+    and the buffer's element count, and the element count against nbytes) are
+    computed without wrapping: a crafted ne whose products wrap to a small
+    value in 64-bit arithmetic must not pass as a 64-element tensor."""
+    t = [wire.TensorDesc(0, 0, 128, "fp16", "row_major", ne),
+         wire.TensorDesc(0, 256, 128, "fp16", "row_major", (ne[0], ne[2], ne[1], ne[3]))]
+    op = wire.OpDesc(KIND_ID["transpose_hd"], (), (0,), (1,))
+    blob = wire.pack_batch([wire.BufDesc(3, 512)], t, [op])
+    sess.mmap(3, 512)
+    assert sess.invoke(blob)[0] == wire.STATUS[want]
+
+
+def test_patchify_extent_with_seven_factors_saturates(sess):
+    """patchify's output extent multiplies seven checked ints; a product past
+    2^128 saturates instead of wrapping."""
+    big = 0x7fffffff
+    t = [wire.TensorDesc(0, 0, 256, "fp32", "row_major", (3, 1, 4, 4)),
+         wire.TensorDesc(0, 256, 256, "fp32", "row_major", (64, 1, 1, 1))]
+    op = wire.OpDesc(KIND_ID["patchify"], (big, big, big, big, 1), (0,), (1,))
+    blob = wire.pack_batch([wire.BufDesc(3, 512)], t, [op])
+    sess.mmap(3, 512)
+    assert sess.invoke(blob)[0] == wire.STATUS["ERR_INVAL_PARAMS"]
+
+
 def test_bad_activation_code_is_refused(sess):
     M, K, N = 4, 64, 32
     sizes = [M * K * 2, K * N // 32 * 18, N * 4, M * N * 2]
