@@ -2174,6 +2174,8 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         const size_t bytes = (size_t) batch * splits * (size_t) p.M * p.N * sizeof(float);
         float *ws = hx::dry_run() ? nullptr : hx::workspace(bytes);
         if (hx::dry_run()) hx::reserve_workspace(bytes);
+        // a caller-fixed workspace too small for this split: launch nothing
+        if (!ws && hx::FixedWorkspace::refused()) return;
         if (ws || hx::dry_run()) {
             p.splits = splits;
             p.k_per_split = per * BK;
@@ -2288,6 +2290,57 @@ extern "C" void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *
     if (!a || !wt || !out || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
     launch<B_NK>(args(a, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act), 1,
                  K % 8 == 0 && hx::aligned(a, 16), K % 8 == 0 && hx::aligned(wt, 16));
+}
+
+// ---- the no-allocation form of matmul_epilogue_f16wt_fp16 ----------------------
+// For callers that cannot allocate (code under graph capture, tight serving
+// loops): the split-K partials live in this file-scope device array -- one
+// copy per GPU, held until the process ends -- instead of the library's
+// grow-only workspace. Host code never uses the array's name as an address:
+// each device's address comes from hipGetSymbolAddress on that device's first
+// call. Every call on one GPU shares that GPU's array; calls that overlap in
+// time on one GPU (different streams, or two graphs replaying at once) race on
+// it. The partials are written in full before they are read, so nothing needs
+// clearing between calls.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t) 16 << 20;
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[16] = {};
+
+// This device's address of `scratch`, looked up once per device (with that
+// device current); nullptr (and the HIP error noted) if the lookup fails.
+float *noalloc_scratch() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 16) return nullptr;
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[d]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            hx::note(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            return nullptr;
+        }
+        g_scratch_ptr[d] = static_cast<float *>(ptr);
+    }
+    return g_scratch_ptr[d];
+}
+}  // namespace
+
+extern "C" int matmul_epilogue_f16wt_noalloc_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
+                                                  hexlib_hf *out, int M, int K, int N, int act) {
+    if (!a || !wt || !out || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return HEXLIB_DSP_ERR_INVAL_PARAMS;
+    float *ws = noalloc_scratch();
+    if (!ws) return HEXLIB_DSP_ERR_INTERNAL;
+    bool refused;
+    {
+        hx::FixedWorkspace fixed(ws, NOALLOC_SCRATCH_BYTES);
+        launch<B_NK>(args(a, K, 0, wt, K, 0, bias, out, N, 0, M, N, K, act), 1,
+                     K % 8 == 0 && hx::aligned(a, 16), K % 8 == 0 && hx::aligned(wt, 16));
+        refused = hx::FixedWorkspace::refused();
+    }
+    return refused ? HEXLIB_DSP_ERR_VTCM_TOO_SMALL : HEXLIB_DSP_OK;
 }
 
 extern "C" void matmul_epilogue_f16wt_res_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,

@@ -34,7 +34,8 @@ void set_current_scratch(Scratch *s);   // nullptr: the process default
 
 // The split-K workspace of at least `bytes` on the current device, from the
 // current scratch, or nullptr when it cannot be had without an allocation
-// during stream capture (the caller then runs without split-K).
+// during stream capture (the caller then runs without split-K) -- or, under a
+// FixedWorkspace, when it does not fit that buffer (refused() then says so).
 float *workspace(size_t bytes);
 // Dry runs record the largest workspace a validated blob will need ...
 void reserve_workspace(size_t bytes);
@@ -42,6 +43,13 @@ void reserve_workspace(size_t bytes);
 // capture). 0 on success.
 int prepare_workspace();
 
+// For the calling thread while alive: workspace() hands out `ptr` (capacity
+// `cap` bytes) and never allocates; a larger request is refused.
+struct FixedWorkspace {
+    FixedWorkspace(float *ptr, size_t cap);
+    ~FixedWorkspace();
+    static bool refused();
+};
 
 inline bool aligned(const void *p, uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;

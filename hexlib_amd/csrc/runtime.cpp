@@ -57,6 +57,9 @@ struct Scratch {
 static Scratch g_default_scratch;
 static thread_local Scratch *t_scratch = nullptr;
 static thread_local size_t t_reserve = 0;
+static thread_local float *t_fixed_ptr = nullptr;
+static thread_local size_t t_fixed_cap = 0;
+static thread_local bool t_fixed_on = false, t_fixed_refused = false;
 
 Scratch *scratch_new() { return new (std::nothrow) Scratch(); }
 
@@ -78,6 +81,11 @@ static int current_device() {
 }
 
 float *workspace(size_t bytes) {
+    if (t_fixed_on) {
+        if (bytes <= t_fixed_cap) return t_fixed_ptr;
+        t_fixed_refused = true;
+        return nullptr;
+    }
     Scratch *s = current_scratch();
     const int d = current_device();
     std::lock_guard<std::mutex> g(s->mu);
@@ -104,6 +112,19 @@ int prepare_workspace() {
     if (!want) return 0;
     return workspace(want) ? 0 : -1;
 }
+
+FixedWorkspace::FixedWorkspace(float *ptr, size_t cap) {
+    t_fixed_ptr = ptr;
+    t_fixed_cap = cap;
+    t_fixed_on = true;
+    t_fixed_refused = false;
+}
+FixedWorkspace::~FixedWorkspace() {
+    t_fixed_on = false;
+    t_fixed_ptr = nullptr;
+    t_fixed_cap = 0;
+}
+bool FixedWorkspace::refused() { return t_fixed_refused; }
 
 }  // namespace hx
 

@@ -48,6 +48,7 @@ SIGNATURES = {
     "rope_2d_qk_fp16": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "hexlib_gpu_gemm_override": (_I, [_I, _I, _I, _I]),
     "hexlib_gpu_attention_override": (_I, [_I]),
+    "matmul_epilogue_f16wt_noalloc_fp16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "hexlib_gpu_set_stream": (None, [_P]),
     "hexlib_gpu_get_stream": (_P, []),
     "hexlib_gpu_take_error": (_I, []),

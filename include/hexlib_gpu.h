@@ -212,6 +212,20 @@ void matmul_epilogue_f16wt_fp16(const hexlib_hf *a, const hexlib_hf *wt,
 void matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *a, const hexlib_hf *wt, const float *bias,
                                      const float *costab, const float *sintab, hexlib_hf *out,
                                      int M, int K, int N, int act, int rope_heads, int rope_dim);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). matmul_epilogue_f16wt_fp16 with the same kernels, tiles
+ * and summation order (bit-identical results), but any split-K partials live
+ * in a fixed 16 MiB per-GPU device array of the library instead of its
+ * grow-only workspace, and nothing is allocated. Returns HEXLIB_DSP_OK;
+ * ERR_INVAL_PARAMS for invalid arguments (the other entry's silent no-op);
+ * ERR_VTCM_TOO_SMALL, before any launch, when the plan's partials
+ * (splits x M x N fp32) exceed the array; ERR_INTERNAL if the array's address
+ * cannot be found. Calls that overlap in time on one GPU share the array and
+ * race. */
+int matmul_epilogue_f16wt_noalloc_fp16(const hexlib_hf *a, const hexlib_hf *wt,
+                                       const float *bias, hexlib_hf *out,
+                                       int M, int K, int N, int act);
 /* fp16(resid + fp16(act(a @ w + bias))), w given transposed as in
  * matmul_epilogue_f16wt_fp16 (KIND 21): a linear followed by the residual
  * add_fp16 that consumes it, each rounded as the reference stores it.
