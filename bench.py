@@ -753,6 +753,11 @@ def main() -> int:
                     help="time the four batch-32 product linears in the plan and torch.matmul on the "
                          "same shapes, print them and exit (the rocprofv3 --pmc target for those GEMMs)")
     ap.add_argument("--no-library", action="store_true", help="with --gemm-b32: skip torch.matmul")
+    ap.add_argument("--plan-only", metavar="VARIANT", choices=("256_b1", "256_b32", "448_b1"),
+                    help="build that plan, time --steps graph replays of it and exit (a rocprofv3 "
+                         "target: every kernel of the plan, nothing else)")
+    ap.add_argument("--copy-ref-first", action="store_true",
+                    help="with --plan-only: first run a plain copy of known size (counter scale)")
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 output directory and exit")
     args = ap.parse_args()
@@ -770,6 +775,21 @@ def main() -> int:
     from hexlib_amd.exec.gpu import GpuPlan, GpuSession
 
     session = GpuSession()
+    if args.plan_only:
+        base = replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
+        vcfg = {"256_b1": base, "256_b32": replace(base, batch=32),
+                "448_b1": replace(E.encoder_at(448), attention="fused_qkv_rope")}[args.plan_only]
+        if args.copy_ref_first:
+            copy_reference()
+        _, _, wbv = build_plan(vcfg)
+        pv = GpuPlan(wbv, session)
+        sec = time_replays(pv, args.steps, args.warmup)
+        pv.close()
+        session.close()
+        print(json.dumps({"plan": args.plan_only, "ops": wbv.n_ops, "steps": args.steps,
+                          "ms_per_step": round(sec / args.steps * 1e3, 4),
+                          "images_per_s": round(args.steps * vcfg.batch / sec, 2)}))
+        return 0
     if args.gemm_b32:
         rows = gemm_b32(session, library=not args.no_library)
         session.close()

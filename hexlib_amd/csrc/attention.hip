@@ -147,16 +147,29 @@ __device__ __forceinline__ void softmax_step(f32x16 (&s)[NSUB], int key0, int T,
             for (int i = 0; i < 16; ++i) oacc[t][i] *= alpha;
         m = m_new;
     }
+    // two copies of the loop under a wave-uniform branch: only the last tile
+    // pays for the key test
     float psum = 0.f;
+    if (part) {
 #pragma unroll
-    for (int u = 0; u < NSUB; ++u)
+        for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][i], c, -m));
-            if (part && key0 + 32 * u + 16 * (i >> 3) + 8 * hl + (i & 7) >= T) p = 0.0f;
-            psum += p;
-            pb[u][i >> 3][i & 7] = (f16) p;
-        }
+            for (int i = 0; i < 16; ++i) {
+                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][i], c, -m));
+                if (key0 + 32 * u + 16 * (i >> 3) + 8 * hl + (i & 7) >= T) p = 0.0f;
+                psum += p;
+                pb[u][i >> 3][i & 7] = (f16) p;
+            }
+    } else {
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][i], c, -m));
+                psum += p;
+                pb[u][i >> 3][i & 7] = (f16) p;
+            }
+    }
     l += psum;
 }
 
@@ -189,7 +202,11 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd(const f16 *__restrict__ q
     const f16 *qb = q + row0 * ldqk + (long long) h * D, *kb = k + row0 * ldqk + (long long) h * D,
               *vb = v + row0 * ldv + (long long) h * D;
     f16 *ob = o + row0 * ldo + (long long) h * D;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
+    // the wave index through readfirstlane: the compiler then knows every
+    // key-tile index derived from it is wave-uniform, so the partial-tile
+    // masking below is a scalar branch, not predicated code on every tile
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, hl = lane >> 5,
+              c32 = lane & 31;
     const int q0 = blockIdx.x * QT;
     f16 *vt = v_all[wave];
     f16 *ktl = k_all[wave];
@@ -365,14 +382,25 @@ __global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ 
     __shared__ __attribute__((aligned(16))) f16 ring[LDS_BYTES / 2];
     __shared__ float part_m[KS > 1 ? W : 1][32], part_l[KS > 1 ? W : 1][32];
 
-    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    // A one-dimensional grid of (image, head, query block) tasks, renumbered
+    // so that each XCD (the hardware deals workgroup i to XCD i % 8) takes a
+    // contiguous run of them: the query blocks of one (image, head) then read
+    // its K and V through one L2. A bijection whatever the dealing.
+    const int nq = (T + 32 * QG - 1) / (32 * QG);
+    const int ntask = gridDim.x, q8 = ntask / 8, r8 = ntask % 8, xcd = blockIdx.x % 8, li = blockIdx.x / 8;
+    const int task = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + li;
+    const int bh = task / nq, qblk = task % nq, b = bh / H, h = bh % H;
     const long long ldo = (long long) H * D, row0 = (long long) b * T;
     const f16 *qb = q + row0 * ldqk + (long long) h * D, *kb = k + row0 * ldqk + (long long) h * D,
               *vb = v + row0 * ldv + (long long) h * D;
     f16 *ob = o + row0 * ldo + (long long) h * D;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
+    // the wave index through readfirstlane: the compiler then knows every
+    // key-tile index derived from it is wave-uniform, so the partial-tile
+    // masking below is a scalar branch, not predicated code on every tile
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, hl = lane >> 5,
+              c32 = lane & 31;
     const int qg = wave % QG, ks = wave / QG;
-    const int q0 = blockIdx.x * (32 * QG) + qg * 32;
+    const int q0 = qblk * (32 * QG) + qg * 32;
     const int n_stages = (T + KS_KEYS - 1) / KS_KEYS, iters = (n_stages + KS - 1) / KS;
     const int tr_off = (8 * hl + ((lane & 15) >> 2)) * V_STRIDE + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     const int krow_key = kperm(c32);
@@ -493,7 +521,7 @@ __global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ 
         __syncthreads();
         for (int e = threadIdx.x; e < QG * 32 * (D / 8); e += 64 * W) {
             const int g = e / (32 * (D / 8)), qq = (e / (D / 8)) % 32, d0 = (e % (D / 8)) * 8;
-            const int qi = blockIdx.x * (32 * QG) + g * 32 + qq;
+            const int qi = qblk * (32 * QG) + g * 32 + qq;
             if (qi >= T) continue;
             float mx = -INFINITY;
 #pragma unroll
@@ -528,7 +556,9 @@ std::atomic<int> g_attn_form{0};
 // attn_qg with QG query groups and KS key splits; false for a form not built.
 bool launch_qg(int qg, int ks, const f16 *Q, const f16 *K, long long ldqk, const f16 *V, long long ldv, f16 *O,
                int T, int H, int D, int batch, float sl2e) {
-    const dim3 grid((unsigned) ((T + 32 * qg - 1) / (32 * qg)), (unsigned) (batch * H));
+    const long long tasks = (long long) ((T + 32 * qg - 1) / (32 * qg)) * batch * H;
+    if (tasks > 0x7fffffffLL) return false;
+    const dim3 grid((unsigned) tasks);
 #define HX_QG(D_, QG_, KS_)                                                                             \
     if (D == D_ && qg == QG_ && ks == KS_) {                                                            \
         HX_LAUNCH((attn_qg<D_, QG_, KS_>), grid, dim3(64 * QG_ * KS_), 0, Q, K, ldqk, V, ldv, O, T, H, sl2e); \
@@ -546,12 +576,16 @@ bool launch_qg(int qg, int ks, const f16 *Q, const f16 *K, long long ldqk, const
 
 // The automatic choice: the shared-K/V form wherever its grid still fills the
 // chip, else 0 (attn_fwd).
-// From a sweep on MI355X (12 heads of 64): 256 tokens at batch 32, 26.6 us
-// against 41.3 (the per-wave-tiles kernel); at 784 and 1024 tokens of one
-// image and at batch 4 the per-wave-tiles kernel is as fast or faster.
+// From a sweep on MI355X (12 heads of 64): 256 tokens at batch 32, 18.6 us
+// against 39.0 (the per-wave-tiles kernel); at 784 and 1024 tokens of one
+// image the per-wave-tiles kernel is as fast (12.1 us, 14.6 us).
 int qg_auto(int T, int H, int batch) {
     const long long heads = (long long) batch * H;
-    return heads * ((T + 127) / 128) >= 2 * CUS ? 41 : 0;
+    if (heads * ((T + 127) / 128) >= 2 * CUS) return 41;
+    // a few images (batch 4: 48 heads): two key splits of two query groups
+    // share each stage (5.8 us against 6.5)
+    if (T <= 512 && heads * ((T + 63) / 64) >= CUS / 2) return 22;
+    return 0;
 }
 
 void launch(const hexlib_hf *q, const hexlib_hf *k, long long ldqk, const hexlib_hf *v, long long ldv,

@@ -1059,67 +1059,81 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
 // K % KW_BK == 0 and 16-byte aligned rows.
 constexpr int KW_BK = 256;
 
-// One 32x32 output block's rope epilogue (the lane holds row m, columns
-// nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order): the same arithmetic as
-// gemm_nk_lds's rope epilogue, with every bias and table load issued first.
-template <int ACT, int RD>
-__device__ __forceinline__ void store_block_rope_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
-    const int rope_d = RD ? RD : p.rope_d;   // RD: the head width fixed at compile time (0: runtime)
-    const int half = rope_d >> 1;
-    const int mc = min(m, p.M - 1);
+// What one lane needs to store its 4 groups of a block with the rope: the
+// groups' rope quads, bias values and table entries. Loaded apart from the
+// store so a kernel can issue the loads early (gemm_nk_kw issues them before
+// its first stage's copies).
+struct RopeBlock {
     RopeQuad q[4];
     bool rope[4];
     float bv[4][4];
     float2 c0[4], c1[4], s0[4], s1[4];
+};
+
+template <int RD>
+__device__ __forceinline__ RopeBlock rope_block_load(const GemmArgs &p, int m, int nb, int lane) {
+    const int rope_d = RD ? RD : p.rope_d;   // RD: the head width fixed at compile time (0: runtime)
+    const int half = rope_d >> 1;
+    const int mc = min(m, p.M - 1);
+    RopeBlock rb;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
-        rope[g] = n < p.rope_cols;
-        q[g] = rope[g] ? rope_quad(n, rope_d) : RopeQuad{n, n + 1, 0};
-        const int f[4] = {q[g].lo, rope[g] ? q[g].hi : n + 1, q[g].lo + (rope[g] ? 1 : 2),
-                          rope[g] ? q[g].hi + 1 : n + 3};
+        rb.rope[g] = n < p.rope_cols;
+        rb.q[g] = rb.rope[g] ? rope_quad(n, rope_d) : RopeQuad{n, n + 1, 0};
+        const int f[4] = {rb.q[g].lo, rb.rope[g] ? rb.q[g].hi : n + 1, rb.q[g].lo + (rb.rope[g] ? 1 : 2),
+                          rb.rope[g] ? rb.q[g].hi + 1 : n + 3};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bv[g][e] = (p.bias && n < p.N) ? p.bias[f[e]] : 0.0f;
-        if (rope[g]) {
-            const long long ld = p.M, o = (long long) q[g].t * ld + mc, oh = o + half * ld;
-            c0[g] = float2{p.rcos[o], p.rcos[o + ld]};
-            c1[g] = float2{p.rcos[oh], p.rcos[oh + ld]};
-            s0[g] = float2{p.rsin[o], p.rsin[o + ld]};
-            s1[g] = float2{p.rsin[oh], p.rsin[oh + ld]};
+        for (int e = 0; e < 4; ++e) rb.bv[g][e] = (p.bias && n < p.N) ? p.bias[f[e]] : 0.0f;
+        rb.c0[g] = rb.c1[g] = rb.s0[g] = rb.s1[g] = float2{0.0f, 0.0f};
+        if (rb.rope[g]) {
+            const long long ld = p.M, o = (long long) rb.q[g].t * ld + mc, oh = o + half * ld;
+            rb.c0[g] = float2{p.rcos[o], p.rcos[o + ld]};
+            rb.c1[g] = float2{p.rcos[oh], p.rcos[oh + ld]};
+            rb.s0[g] = float2{p.rsin[o], p.rsin[o + ld]};
+            rb.s1[g] = float2{p.rsin[oh], p.rsin[oh + ld]};
         }
     }
+    return rb;
+}
+
+template <int ACT>
+__device__ __forceinline__ void rope_block_store(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v,
+                                                 const RopeBlock &rb) {
     if (m >= p.M) return;
     f16 *crow = p.C + (long long) m * p.ldc;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
         if (n >= p.N) continue;
-        if (rope[g]) {
+        if (rb.rope[g]) {
             float x[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = f32_rounded(act_t<ACT>(v[g * 4 + e] + bv[g][e]));
-            rope_store4(crow, q[g], x, c0[g], c1[g], s0[g], s1[g]);
+            for (int e = 0; e < 4; ++e) x[e] = f32_rounded(act_t<ACT>(v[g * 4 + e] + rb.bv[g][e]));
+            rope_store4(crow, rb.q[g], x, rb.c0[g], rb.c1[g], rb.s0[g], rb.s1[g]);
         } else {
             f16x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, false>(v[g * 4 + e] + bv[g][e], (f16) 0);
+            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, false>(v[g * 4 + e] + rb.bv[g][e], (f16) 0);
             *reinterpret_cast<f16x4 *>(crow + n) = o;
         }
     }
 }
 
+// One 32x32 output block's rope epilogue (the lane holds row m, columns
+// nb + 8 g + 4 (lane / 32) .. + 3 in MFMA order): the same arithmetic as
+// gemm_nk_lds's rope epilogue, with every bias and table load issued first.
 // The encoder's head width (64) gets its own form: the column-to-pair mapping
 // then takes shifts and masks instead of integer divisions.
-__device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v) {
-    if (p.rope_d == 64) {
-        if (p.act == 1) store_block_rope_t<1, 64>(p, m, nb, lane, v);
-        else if (p.act == 2) store_block_rope_t<2, 64>(p, m, nb, lane, v);
-        else store_block_rope_t<0, 64>(p, m, nb, lane, v);
-    } else {
-        if (p.act == 1) store_block_rope_t<1, 0>(p, m, nb, lane, v);
-        else if (p.act == 2) store_block_rope_t<2, 0>(p, m, nb, lane, v);
-        else store_block_rope_t<0, 0>(p, m, nb, lane, v);
-    }
+__device__ __forceinline__ RopeBlock load_block_rope(const GemmArgs &p, int m, int nb, int lane) {
+    return p.rope_d == 64 ? rope_block_load<64>(p, m, nb, lane) : rope_block_load<0>(p, m, nb, lane);
+}
+
+__device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v,
+                                                 const RopeBlock &rb) {
+    if (p.act == 1) rope_block_store<1>(p, m, nb, lane, v, rb);
+    else if (p.act == 2) rope_block_store<2>(p, m, nb, lane, v, rb);
+    else rope_block_store<0>(p, m, nb, lane, v, rb);
 }
 
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
@@ -1203,6 +1217,13 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     // output block, issued now, ahead of the ring's first copies
     BlockBias bbias{};
     BlockRes bres{};
+    // the rope epilogue's bias and tables for the block this wave stores (block
+    // `wave`), likewise issued before the ring
+    RopeBlock rblk{};
+    if constexpr (ROPE) {
+        if (wave < NB * NB)
+            rblk = load_block_rope(p, m0 + (wave / NB) * 32 + (lane & 31), n0 + (wave % NB) * 32, lane);
+    }
     if constexpr (!ROPE) {
         bbias = load_block_bias(p, n0 + (wave % NB) * 32);
         if (p.R && wave < NB * NB) {
@@ -1317,7 +1338,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     // lane l holds output row l % 32 of the block, columns 8 g + 4 (l / 32) .. + 3
     const int m = m0 + (blk / NB) * 32 + r;
     if constexpr (ROPE) {   // the rope entry point's guarantees: N % 4, rope_d % 4, ldc == N, no residual
-        store_block_rope(p, m, n0 + (blk % NB) * 32, lane, sum);
+        store_block_rope(p, m, n0 + (blk % NB) * 32, lane, sum, rblk);
         return;
     }
     if (m >= p.M) return;
@@ -1965,13 +1986,20 @@ bool launch_big(const GemmArgs &p, Tile t, int stages) {
 }
 
 // The large-tile kernel's tile for an M x N product, or {0, 0} for the other
-// paths. From a sweep of every form on MI355X: the 128 x 128 tile with a
-// 2-slice ring (64 KB of LDS, two workgroups per CU) is the fastest form on
-// the encoder's batch-32 shapes -- 8192 x 768 x 3072 81 us against 96 us,
-// 8192 x 3072 x 768 59 against 74, 8192 x 768 x 768 28 against 33 -- wherever
-// its grid fills at least one round of 256 workgroups; with fewer tiles
-// (784 rows, 2048 x 3072 x 1024) the other paths are faster.
-Tile big_auto(int M, int N) {
+// paths. From a sweep of every form on MI355X at the encoder's batch-32 shapes
+// (M = 8192, GELU epilogue, N(0, 1) operands): the 128 x 192 tile with a
+// 2-slice ring (80 KB of LDS, two workgroups per CU) is the fastest plain
+// linear wherever N % 192 == 0 -- 8192 x 768 x 3072 54.4 us against 56.3 for
+// 128 x 128, 8192 x 3072 x 768 46.9 against 49.2, 8192 x 768 x 2304 41.3
+// against 46.0. With the residual epilogue it is slower (8192 x 768 x 768 in
+// the plan: 22.5 us against 19.7; its 24 chunks per row leave 16 threads of
+// each sweep idle), and the rope epilogue exists in the 128 x 128 form: those
+// take 128 x 128. Both wherever the grid fills at least one round of 256
+// workgroups; with fewer tiles (784 rows, 2048 x 3072 x 1024) the other paths
+// are faster.
+Tile big_auto(int M, int N, bool plain) {
+    const long long t192 = (long long) ((M + 127) / 128) * ((N + 191) / 192);
+    if (plain && N % 192 == 0 && t192 >= 256) return Tile{128, 192};
     const long long tiles = (long long) ((M + 127) / 128) * ((N + 127) / 128);
     return tiles >= 256 ? Tile{128, 128} : Tile{0, 0};
 }
@@ -2083,7 +2111,7 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
                         (!p.rcos || (p.rope_d == BIG_RD && p.rope_cols % 8 == 0 && !p.R && p.M % 4 == 0 &&
                                      ((uintptr_t) p.rcos & 15) == 0 && ((uintptr_t) p.rsin & 15) == 0));
     if (big_ok && (path == 5 || path == 0)) {
-        const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N);
+        const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N, !p.rcos && !p.R);
         const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;
         if (bt.bm && launch_big(p, bt, stages)) return;
     }
