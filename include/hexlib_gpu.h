@@ -9,7 +9,7 @@
  *     dimensions make the call a silent no-op, as in the reference.
  *  2. The entry adapters `int <kernel>_entry(const hexlib_args *)` and the
  *     dispatch table `hexlib_kernel_table[]`, keyed by the reference's wire
- *     KIND_ID (1-12) plus appended ids 13-23. Generated from the host's
+ *     KIND_ID (1-12) plus appended ids 13-25. Generated from the host's
  *     RunnerSpec table (hexlib_amd/exec/genentry.py).
  *  3. A session with the reference IDL's lifecycle (open/start/mmap/invoke/
  *     stop/close/hwinfo) that validates a batch blob on the host, resolves
