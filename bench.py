@@ -753,7 +753,8 @@ def main() -> int:
                     help="time the four batch-32 product linears in the plan and torch.matmul on the "
                          "same shapes, print them and exit (the rocprofv3 --pmc target for those GEMMs)")
     ap.add_argument("--no-library", action="store_true", help="with --gemm-b32: skip torch.matmul")
-    ap.add_argument("--plan-only", metavar="VARIANT", choices=("256_b1", "256_b32", "448_b1"),
+    ap.add_argument("--plan-only", metavar="VARIANT",
+                    choices=("256_b1", "256_b32", "448_b1", "256_b1_q8_0", "256_b1_q4_0"),
                     help="build that plan, time --steps graph replays of it and exit (a rocprofv3 "
                          "target: every kernel of the plan, nothing else)")
     ap.add_argument("--copy-ref-first", action="store_true",
@@ -778,7 +779,9 @@ def main() -> int:
     if args.plan_only:
         base = replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
         vcfg = {"256_b1": base, "256_b32": replace(base, batch=32),
-                "448_b1": replace(E.encoder_at(448), attention="fused_qkv_rope")}[args.plan_only]
+                "448_b1": replace(E.encoder_at(448), attention="fused_qkv_rope"),
+                "256_b1_q8_0": replace(E.QWEN35_VISION_Q8, attention="fused_qkv_rope"),
+                "256_b1_q4_0": replace(E.QWEN35_VISION_Q4, attention="fused_qkv_rope")}[args.plan_only]
         if args.copy_ref_first:
             copy_reference()
         _, _, wbv = build_plan(vcfg)

@@ -1150,7 +1150,8 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
 template <int T, bool ROPE = false, bool KN = false, int QB = 0>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
-    static_assert(QB == 0 || (!KN && !ROPE && (QB == 8 || QB == 4)), "quantized weights come as W^T blocks");
+    static_assert(QB == 0 || (!ROPE && (QB == 8 || QB == 4) && (!KN || QB == 4)),
+                  "quantized weights: q8_0 / q4_0 blocks along K of W^T, or q4_0 blocks along N of [K][N]");
     constexpr bool Q8 = QB != 0;                 // a block-quantized weight (either format)
     constexpr int QBYTES = QB == 8 ? 34 : 18;
     constexpr int NB = T / 32;                 // 32-row blocks per tile side
@@ -1175,7 +1176,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             else lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
-    // q8_0: a stage is T rows x 8 blocks; thread t takes blocks t + 256 u
+    // blocks along K of W^T: a stage is T rows x 8 blocks; along N of [K][N]
+    // (KN, T = 64): 256 k x 2 blocks. Thread t takes blocks t + 256 u.
     constexpr int NQ = Q8 ? T * 8 / TPB : 1;
     struct Q8Regs {
         float d[NQ];
@@ -1186,6 +1188,11 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
+            if constexpr (KN) {   // block (k, n0 / 32 + (b & 1)), k = kt * 256 + b / 2
+                load_q4_block(Bq + (long long) (kt * KW_BK + (b >> 1)) * p.ldb + (n0 / 32 + (b & 1)) * 18, q.d[u],
+                              q.qs[u]);
+                continue;
+            }
             const uint8_t *src = Bq + (long long) min(n0 + row, p.N - 1) * p.ldb + (kt * 8 + kb) * QBYTES;
             if constexpr (QB == 8) {
                 load_q8_half(src, 0, q.d[u], q.qs[u]);
@@ -1200,6 +1207,20 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
+            if constexpr (KN) {
+                // the block's 32 values are n = n0 + 32 (b & 1) + j of row k:
+                // four 8-column chunks of that k row of the [64 k][64 n] sub-slice
+                const int kr = (b >> 1) & 63, nb = b & 1;
+                f16 *drow = sB[st][(b >> 1) >> 6] + kr * DS_ROW;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    f16x8 v;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = q4_val(q.d[u], nib(q.qs[u], (c * 8 + j) & 15, ((c * 8 + j) >> 4) * 4));
+                    *reinterpret_cast<f16x8 *>(drow + (((nb * 4 + c) ^ swz(kr)) << 3)) = v;
+                }
+                continue;
+            }
             f16 *dst = sB[st][kb >> 1] + row * DS_ROW;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -1275,20 +1296,47 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         // multiplies stage kt, then dequantizes stage kt + 1 into its slot --
         // free, since every wave has passed this iteration's barrier after
         // multiplying stage kt + 1 - STAGES.
-        Q8Regs q8r;
-        q8_load(0, q8r);
-        q8_store(0, q8r);
-        for (int kt = 0; kt < KT; ++kt) {
-            const int st = kt % STAGES;
-            HX_WAIT_VMCNT(0);
-            HX_WAIT_LGKM0();
-            __builtin_amdgcn_s_barrier();
-            if (kt + 1 < KT) {
-                if (kt + 1 >= (FULL ? STAGES : STAGES - 1)) issue(kt + 1, (kt + 1) % STAGES);   // else the prologue sent it
-                q8_load(kt + 1, q8r);
+        Q8Regs qx, qy;
+        q8_load(0, qx);
+        if (KT <= 3) {
+            q8_store(0, qx);
+            for (int kt = 0; kt < KT; ++kt) {
+                const int st = kt % STAGES;
+                HX_WAIT_VMCNT(0);
+                HX_WAIT_LGKM0();
+                __builtin_amdgcn_s_barrier();
+                if (kt + 1 < KT) {
+                    if (kt + 1 >= (FULL ? STAGES : STAGES - 1)) issue(kt + 1, (kt + 1) % STAGES);   // else the prologue sent it
+                    q8_load(kt + 1, qx);
+                }
+                mma_stage(st);
+                if (kt + 1 < KT) q8_store((kt + 1) % STAGES, qx);
             }
-            mma_stage(st);
-            if (kt + 1 < KT) q8_store((kt + 1) % STAGES, q8r);
+        } else {
+            // Longer K: the blocks are loaded a stage earlier than they are
+            // dequantized -- stage s in register set s % 2, stage kt + 2's
+            // blocks sent in iteration kt ahead of stage kt + 1's A copies --
+            // so the wait at the top of iteration kt + 1, needed for those
+            // copies anyway, has them in registers before stage kt + 2 is
+            // dequantized at its end (256 x 3072 x 768 q8_0: 13.5 us
+            // against 14.2; at K = 768 the form above measured faster).
+            q8_load(1, qy);
+            q8_store(0, qx);
+            auto step = [&](int kt, Q8Regs &cur, const Q8Regs &nxt) {   // cur: stage kt (done), nxt: kt + 1
+                const int st = kt % STAGES;
+                HX_WAIT_VMCNT(0);
+                HX_WAIT_LGKM0();
+                __builtin_amdgcn_s_barrier();
+                if (kt + 2 < KT) q8_load(kt + 2, cur);
+                if (kt + 1 < KT && kt + 1 >= (FULL ? STAGES : STAGES - 1))
+                    issue(kt + 1, (kt + 1) % STAGES);   // else the prologue sent it
+                mma_stage(st);
+                if (kt + 1 < KT) q8_store((kt + 1) % STAGES, nxt);
+            };
+            for (int kt = 0; kt < KT; kt += 2) {
+                step(kt, qx, qy);
+                if (kt + 1 < KT) step(kt + 1, qy, qx);
+            }
         }
     } else {
     for (int kt = 0; kt < KT; ++kt) {
@@ -2145,6 +2193,20 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
             HX_LAUNCH((gemv_q<MODE == B_Q8K ? 8 : 4>), dim3((unsigned) ((p.N + WPB - 1) / WPB)), dim3(TPB), 0, p);
             return;
         }
+    }
+    // q4_0 blocked along N (the reference ABI, [K][N/32] blocks) at few rows: the
+    // 64x64 K-across-waves kernel in its [K][N] form, each stage's blocks
+    // dequantized into the ring in the layout its fp16 copies fill. Where the
+    // 32x32 tile would be the choice (N = 768) only up to K = 768, as for the
+    // fp16 [K][N] weight: 256 x 768 x 768 9.8 us against 14.1 on the
+    // register-staged kernel, 256 x 3072 x 768 25.2 against 18.6.
+    const bool kw_q4n_ok = MODE == B_Q4N && batch == 1 && p.K % KW_BK == 0 && p.N % 64 == 0 && p.lda % 8 == 0 &&
+                           avec && (p.M + 63) / 64 <= 65535 && !p.rcos && !p.ln_w && path != 1;
+    const int kw_q4n_auto = kw_auto(p.M, p.N);
+    if (kw_q4n_ok && (path == 4 || (path == 0 && (kw_q4n_auto == 64 || (kw_q4n_auto == 32 && p.K <= 768))))) {
+        HX_LAUNCH((gemm_nk_kw<64, false, true, 4>), dim3((unsigned) (p.N / 64), (unsigned) ((p.M + 63) / 64)),
+                  dim3(TPB), 0, p);
+        return;
     }
     const bool kw_q_ok = (MODE == B_Q8K || MODE == B_Q4K) && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 &&
                          avec && (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w && path != 1;
