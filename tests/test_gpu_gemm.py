@@ -10,6 +10,7 @@ import pytest
 
 from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked
 from oracle import kernels as K
+from oracle.quant import dequantize_q4_0_fp16
 from tests.gpu_util import Dev, h16, report
 
 pytestmark = pytest.mark.gpu
@@ -68,6 +69,38 @@ def test_matmul_epilogue_q4_nblocked(dev, M, Kd, N, act):
     got, want = dev.down(do), K.matmul_epilogue_fp16(a, wq, bias, Kd, N, act)
     report(f"q4n {M}x{Kd}x{N} act{act}", got, want)
     assert K.close_f16(got, want, 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 2304, 0), (256, 768, 768, 1), (256, 768, 3072, 1),
+                                        (70, 512, 128, 2), (1, 256, 64, 0), (300, 1024, 192, 0)])
+def test_q4_nblocked_kw_path(dev, M, Kd, N, act):
+    """The reference-ABI q4_0 weight (blocks along N) on the K-across-waves
+    kernel's [K][N] form (override path 4, and the automatic route at these
+    shapes) is bit-identical to the same kernel's fp16 [K][N] form on the
+    dequantized weight, and within the epilogue tolerance of the oracle and of
+    the register-staged kernel (path 1)."""
+    a, w, bias = _q4_inputs(M, Kd, N, 17)
+    wq = pack_q4_0_nblocked(w)
+    wd = h16(dequantize_q4_0_fp16(wq, (Kd, N)))
+    da, dw, db, dwd = dev.up(a), dev.up(np.frombuffer(wq, np.uint8)), dev.up(bias), dev.up(wd)
+    outs = []
+    for ov, dense in (((64, 64, 0, 4), False), ((0, 0, 0, 0), False), ((0, 0, 1, 1), False), ((64, 64, 0, 4), True)):
+        do = dev.empty((M, N), np.float16)
+        assert dev.lib.hexlib_gpu_gemm_override(*ov) == 1
+        try:
+            if dense:
+                dev.lib.matmul_epilogue_f16w_fp16(dev.ptr(da), dev.ptr(dwd), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+            else:
+                dev.lib.matmul_epilogue_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(do), M, Kd, N, act)
+            dev.check()
+        finally:
+            dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+        outs.append(dev.down(do))
+    np.testing.assert_array_equal(outs[0].view(np.uint16), outs[3].view(np.uint16))
+    np.testing.assert_array_equal(outs[1].view(np.uint16), outs[3].view(np.uint16))
+    want = K.matmul_epilogue_fp16(a, wq, bias, Kd, N, act)
+    assert K.close_f16(outs[0], want, 0.01, 3e-4).all()
+    assert K.close_f16(outs[2], want, 0.01, 3e-4).all()
 
 
 @pytest.mark.parametrize("M,Kd,N", [(1, 896, 4864), (16, 896, 4864), (256, 896, 4864),
