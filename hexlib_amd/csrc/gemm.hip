@@ -2065,6 +2065,83 @@ void launch_lds_rope(const GemmArgs &p, Tile t) {
     else HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, true>), grid, dim3(TPB), 0, p);
 }
 
+// Up to 16 rows on K-grouped quantized weights (QB = 4: q4_0, QB = 8: q8_0):
+// v_mfma_f32_16x16x32_f16 tiles, one 32-k block per MFMA. A workgroup owns 16
+// output columns and NW waves split K into contiguous runs of blocks. Lane l
+// holds the MFMA operands of row / column l % 16 at k = 8 (l / 16) .. + 7: for
+// the weight that is 8 codes of one block of row n of W^T -- q4_0: bytes
+// 8 (c & 1) .. + 7 of the nibbles, low nibbles for c < 2, high otherwise (block
+// element e is byte e & 15's nibble e / 16); q8_0: bytes 8 c .. + 7 -- loaded
+// with the block's scale and dequantized to fp16(d * (q - 8)) or fp16(d * q), as
+// every other path does. PF blocks per wave are in flight. The waves' 16 x 16
+// fp32 partial tiles are summed through LDS in wave order, then bias and
+// activation (`epi`). Needs K % 32 == 0 and 16-byte aligned A rows; rows past M
+// and columns past N are read from a clamped row and never stored.
+template <int QB, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_q16(GemmArgs p) {
+    constexpr int QBYTES = QB == 8 ? 34 : 18, PF = 8;
+    __shared__ float red[NW][64][4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rr = lane & 15, c = lane >> 4;
+    const int n0 = blockIdx.x * 16, n = n0 + rr;
+    const int KB = p.K / 32;
+    const int per = (KB + NW - 1) / NW, b0 = wave * per, nb = max(0, min(per, KB - b0));
+    const uint16_t *wrow = reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(p.B) +
+                                                              (long long) min(n, p.N - 1) * p.ldb);
+    const f16 *arow = p.A + (long long) min(rr, p.M - 1) * p.lda + 8 * c;
+    const float bias = p.bias ? p.bias[min(n, p.N - 1)] : 0.0f;
+    // 16-bit word offsets within a block: the scale, then the lane's 8 code bytes
+    constexpr int BW = QBYTES / 2;
+    const int qw = 1 + (QB == 8 ? 4 * c : 4 * (c & 1));
+    struct Blk {
+        f16x8 a;
+        uint32_t q[2];
+        uint16_t d;
+    };
+    auto load = [&](int b, Blk &x) {
+        const uint16_t *w = wrow + (long long) b * BW;
+        x.d = w[0];
+        x.q[0] = (uint32_t) w[qw] | ((uint32_t) w[qw + 1] << 16);
+        x.q[1] = (uint32_t) w[qw + 2] | ((uint32_t) w[qw + 3] << 16);
+        x.a = *reinterpret_cast<const f16x8 *>(arow + 32 * b);
+    };
+    f32x4 acc = {};
+    Blk buf[PF];
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (u < nb) load(b0 + u, buf[u]);
+    const int sh = QB == 8 ? 0 : 4 * (c >> 1);
+    for (int s0 = 0; s0 < nb; s0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int sidx = s0 + u;
+            if (sidx >= nb) break;
+            const float d = (float) __builtin_bit_cast(f16, buf[u].d);
+            f16x8 wv;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t byte = (buf[u].q[j >> 2] >> (8 * (j & 3))) & 0xFF;
+                if constexpr (QB == 8) wv[j] = (f16) (d * (float) (int8_t) byte);
+                else wv[j] = q4_val(d, (int) ((byte >> sh) & 0xF));
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(buf[u].a, wv, acc, 0, 0, 0);
+            if (sidx + PF < nb) load(b0 + sidx + PF, buf[u]);
+        }
+    }
+    // lane l holds D[4 (l / 16) + i][l % 16] = out[m][n0 + l % 16]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][lane][i] = acc[i];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][lane][i];
+        const int m = 4 * c + i;
+        if (m < p.M && n < p.N) p.C[(long long) m * p.ldc + n] = epi(v + bias, p.act, false, (f16) 0);
+    }
+}
+
 // Few-row GEMM on K-grouped quantized weights (QB = 4: q4_0, 18-byte blocks;
 // QB = 8: q8_0, 34-byte blocks): one wave per output column n. The wave's
 // lanes walk the K/32 blocks of row n of W^T (one contiguous run of bytes),
@@ -2187,6 +2264,21 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     // against 10.0; at M = 4 it is still ahead for K >= 896 (896 x 4864 8.5
     // against 13.6) and behind at K = 768 (5.9 against 5.4).
     if constexpr (MODE == B_Q8K || MODE == B_Q4K) {
+        // the 16-row MFMA kernel: on the automatic route past gemv_q's rows and
+        // where its 16-column workgroups fill a round of CUs (cfg 5's
+        // 896 x 4864 at M = 16: 5.9 us against 13.4; with N = 896 or 2048 its
+        // workgroups are too few and the other routes stay ahead)
+        const bool q16_auto = p.M > GEMV_M && (p.N + 15) / 16 >= 256;
+        if ((path == 7 || (path == 0 && q16_auto)) && batch == 1 && p.M <= 16 && p.K % 32 == 0 && p.lda % 8 == 0 &&
+            avec && !p.rcos && !p.ln_w) {
+            constexpr int QBM = MODE == B_Q8K ? 8 : 4;
+            const dim3 grid((unsigned) ((p.N + 15) / 16));
+            const int nw = path == 7 && g_ov_splits.load() ? g_ov_splits.load() : 8;
+            if (nw == 4) HX_LAUNCH((gemm_q16<QBM, 4>), grid, dim3(256), 0, p);
+            else if (nw == 16) HX_LAUNCH((gemm_q16<QBM, 16>), grid, dim3(1024), 0, p);
+            else HX_LAUNCH((gemm_q16<QBM, 8>), grid, dim3(512), 0, p);
+            return;
+        }
         if (path == 0 && batch == 1 && (p.M <= 2 || (p.M <= GEMV_M && p.K >= 896)) && p.K % 32 == 0 &&
             p.lda % 8 == 0 && avec && !p.rcos && !p.ln_w) {
             constexpr int WPB = TPB / HX_WAVE;
@@ -2350,7 +2442,8 @@ extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
                                          (bm == 128 && bn == 128) || (bm == 64 && bn == 64) ||
                                          (bm == 32 && bn == 64) || (bm == 64 && bn == 32) ||
                                          (path == 3 && bm == 32 && bn == 32);
-    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 5 ||
+    if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 7 || path == 6 ||
+        (path == 7 && (bm || bn || (splits && splits != 4 && splits != 8 && splits != 16))) ||
         (path == 5 && splits > 3))
         return HEXLIB_DSP_ERR_INVAL_PARAMS;
     g_ov_bm = bm;

@@ -329,8 +329,10 @@ const char *hexlib_gpu_status_name(int status);
  * K % 256 == 0 (tile 64x64 selects its 64x64 form, else 32x32), 5 = the
  * large-tile kernel with bm in {128, 256} and bn in {128, 192, 256}, where
  * `splits` is its ring depth instead (0 = 2, at most 3; a form not built falls
- * back to the automatic choice); 2 to 5 apply where their preconditions
- * hold). Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
+ * back to the automatic choice), 7 = the 16-row MFMA kernel for K-grouped
+ * q4_0 / q8_0 weights at up to 16 rows (tile 0x0; `splits` its wave count,
+ * 4, 8 or 16, 0 = 8); 2 to 5 and 7 apply where their preconditions hold).
+ * Returns HEXLIB_DSP_OK or ERR_INVAL_PARAMS. */
 int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path);
 /* Tuning override (no reference counterpart) for the attention kernels'
  * form, for every later attention launch in the process: 0 = automatic,

@@ -248,7 +248,8 @@ def test_forced_split_batched_matmul(dev, splits):
 
 def test_override_rejects_bad_values(dev):
     for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 6), (256, 256, 0, 0),
-                 (32, 128, 0, 3), (128, 32, 0, 3), (64, 64, 0, 5), (256, 256, 4, 5), (192, 256, 0, 5)]:
+                 (32, 128, 0, 3), (128, 32, 0, 3), (64, 64, 0, 5), (256, 256, 4, 5), (192, 256, 0, 5),
+                 (64, 64, 0, 7), (0, 0, 2, 7), (0, 0, 12, 7), (0, 0, 0, 6), (0, 0, 0, 8)]:
         assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
     assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
 
@@ -784,6 +785,42 @@ def test_gemv_quantized_path(dev, qb, M, Kd, N, act):
     want = K.matmul_q4k(a, wq, bias, Kd, N, act) if qb == 4 else K.matmul_q8k(a, wq, bias, Kd, N, act)
     assert K.close_f16(got, want, 0.01, 3e-4).all()
     assert K.close_f16(got, dev.down(d2), 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("qb", [4, 8])
+@pytest.mark.parametrize("M,Kd,N,act", [(16, 896, 4864, 0), (16, 4864, 896, 0), (16, 2048, 2048, 1),
+                                        (1, 2048, 2048, 0), (5, 1024, 100, 2), (11, 96, 40, 0), (16, 32, 17, 1)])
+def test_q16_mfma_quantized_path(dev, qb, M, Kd, N, act):
+    """q4_0 (K-grouped) and q8_0 weights at up to 16 rows on the 16x16x32 MFMA
+    kernel (override path 7): BASELINE cfg 5's shapes at M = 16, ragged M and
+    N, a one-block K: within the harness tolerance of the oracle and of the
+    register-staged kernel (path 1)."""
+    r = rng(47 + qb)
+    blk = 18 if qb == 4 else 34
+    n_blocks = N * Kd // 32
+    blocks = np.empty((n_blocks, blk), np.uint8)
+    blocks[:, :2] = r.uniform(0.005, 0.02, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = r.integers(0, 256, (n_blocks, blk - 2), dtype=np.uint8)
+    wq = blocks.tobytes()
+    a = h16(r.standard_normal((M, Kd)))
+    bias = (0.02 * r.standard_normal(N)).astype(np.float32)
+    da, dq, db = dev.up(a), dev.up(blocks), dev.up(bias)
+    fn = dev.lib.matmul_epilogue_q4k_fp16 if qb == 4 else dev.lib.matmul_epilogue_q8k_fp16
+    outs = {}
+    try:
+        for nw, path in ((4, 7), (8, 7), (16, 7), (0, 1)):   # wave counts of the 16-row kernel; register-staged
+            d = dev.empty((M, N), np.float16)
+            assert dev.lib.hexlib_gpu_gemm_override(0, 0, nw, path) == 1
+            fn(dev.ptr(da), dev.ptr(dq), dev.ptr(db), dev.ptr(d), M, Kd, N, act)
+            dev.check()
+            outs[nw] = dev.down(d)
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    want = K.matmul_q4k(a, wq, bias, Kd, N, act) if qb == 4 else K.matmul_q8k(a, wq, bias, Kd, N, act)
+    for nw in (4, 8, 16):
+        report(f"q16x{nw} q{qb} {M}x{Kd}x{N}", outs[nw], want)
+        assert K.close_f16(outs[nw], want, 0.01, 3e-4).all()
+        assert K.close_f16(outs[nw], outs[0], 0.01, 3e-4).all()
 
 
 @pytest.mark.parametrize("tile", [32, 64])
