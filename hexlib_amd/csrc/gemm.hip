@@ -2077,14 +2077,18 @@ void launch_lds_rope(const GemmArgs &p, Tile t) {
 // fp32 partial tiles are summed through LDS in wave order, then bias and
 // activation (`epi`). Needs K % 32 == 0 and 16-byte aligned A rows; rows past M
 // and columns past N are read from a clamped row and never stored.
-template <int QB, int NW>
+// SPLIT: K is split over gridDim.y workgroups as well, each taking
+// p.k_per_split of it and storing its fp32 partial tile to p.ws [split][M][N]
+// for splitk_reduce (bias, activation) -- where N gives too few workgroups.
+template <int QB, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW) void gemm_q16(GemmArgs p) {
     constexpr int QBYTES = QB == 8 ? 34 : 18, PF = 8;
     __shared__ float red[NW][64][4];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rr = lane & 15, c = lane >> 4;
     const int n0 = blockIdx.x * 16, n = n0 + rr;
-    const int KB = p.K / 32;
-    const int per = (KB + NW - 1) / NW, b0 = wave * per, nb = max(0, min(per, KB - b0));
+    const int kb_lo = SPLIT ? blockIdx.y * (p.k_per_split / 32) : 0;
+    const int KB = SPLIT ? min(p.K / 32, kb_lo + p.k_per_split / 32) : p.K / 32;
+    const int per = (KB - kb_lo + NW - 1) / NW, b0 = kb_lo + wave * per, nb = max(0, min(per, KB - b0));
     const uint16_t *wrow = reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(p.B) +
                                                               (long long) min(n, p.N - 1) * p.ldb);
     const f16 *arow = p.A + (long long) min(rr, p.M - 1) * p.lda + 8 * c;
@@ -2138,7 +2142,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_q16(GemmArgs p) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) v += red[w][lane][i];
         const int m = 4 * c + i;
-        if (m < p.M && n < p.N) p.C[(long long) m * p.ldc + n] = epi(v + bias, p.act, false, (f16) 0);
+        if (m >= p.M || n >= p.N) continue;
+        if constexpr (SPLIT) p.ws[((long long) blockIdx.y * p.M + m) * p.N + n] = v;
+        else p.C[(long long) m * p.ldc + n] = epi(v + bias, p.act, false, (f16) 0);
     }
 }
 
@@ -2264,16 +2270,44 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     // against 10.0; at M = 4 it is still ahead for K >= 896 (896 x 4864 8.5
     // against 13.6) and behind at K = 768 (5.9 against 5.4).
     if constexpr (MODE == B_Q8K || MODE == B_Q4K) {
-        // the 16-row MFMA kernel: on the automatic route past gemv_q's rows and
+        // the 16-row MFMA kernel: on the automatic route past gemv_q's rows,
         // where its 16-column workgroups fill a round of CUs (cfg 5's
-        // 896 x 4864 at M = 16: 5.9 us against 13.4; with N = 896 or 2048 its
-        // workgroups are too few and the other routes stay ahead)
-        const bool q16_auto = p.M > GEMV_M && (p.N + 15) / 16 >= 256;
+        // 896 x 4864 at M = 16: 5.7 us against 13.3) and, with K split over
+        // workgroups, where they are fewer than 64 (4864 x 896: 10.8 against
+        // 13.8); in between (2048 x 2048: 128) the other routes measured as
+        // fast or faster
+        const int q16_gx = (p.N + 15) / 16;
+        const bool q16_auto = p.M > GEMV_M && (q16_gx >= 256 || q16_gx < 64);
         if ((path == 7 || (path == 0 && q16_auto)) && batch == 1 && p.M <= 16 && p.K % 32 == 0 && p.lda % 8 == 0 &&
             avec && !p.rcos && !p.ln_w) {
             constexpr int QBM = MODE == B_Q8K ? 8 : 4;
-            const dim3 grid((unsigned) ((p.N + 15) / 16));
+            const int gx = (p.N + 15) / 16;
             const int nw = path == 7 && g_ov_splits.load() ? g_ov_splits.load() : 8;
+            // fewer than a round of workgroups: split K over up to 8 of them,
+            // at least 8 blocks per wave-run of each
+            int ks = gx >= 256 ? 1 : min(8, (256 + gx - 1) / gx);
+            ks = max(1, min(ks, p.K / 32 / 16));
+            float *ws = nullptr;
+            if (ks > 1) {
+                const int kb = (p.K / 32 + ks - 1) / ks;
+                p.k_per_split = kb * 32;
+                ks = (p.K / 32 + kb - 1) / kb;
+                const size_t bytes = (size_t) ks * p.M * p.N * sizeof(float);
+                ws = hx::dry_run() ? nullptr : hx::workspace(bytes);
+                if (hx::dry_run()) hx::reserve_workspace(bytes);
+                if (!ws && hx::FixedWorkspace::refused()) return;
+                if (!ws && !hx::dry_run()) ks = 1;
+                p.ws = ws;
+            }
+            if (ks > 1) {
+                const dim3 grid((unsigned) gx, (unsigned) ks);
+                HX_LAUNCH((gemm_q16<QBM, 8, true>), grid, dim3(512), 0, p);
+                HX_LAUNCH(splitk_reduce, dim3(hx::blocks_for(((long long) p.M * p.N + 3) / 4, TPB, 4096)), dim3(TPB),
+                          0, (const float *) p.ws, p.bias, p.C, p.ldc, 0LL, p.M, p.N, ks, p.act, 1,
+                          (const f16 *) nullptr, 0LL);
+                return;
+            }
+            const dim3 grid((unsigned) gx);
             if (nw == 4) HX_LAUNCH((gemm_q16<QBM, 4>), grid, dim3(256), 0, p);
             else if (nw == 16) HX_LAUNCH((gemm_q16<QBM, 16>), grid, dim3(1024), 0, p);
             else HX_LAUNCH((gemm_q16<QBM, 8>), grid, dim3(512), 0, p);
