@@ -1424,66 +1424,62 @@ __device__ __forceinline__ void interleave_reads() {
     }
 }
 
-// The rope form's epilogue (BM = BN = 128, rope_d = 64) stages, per pass, the
-// rope tables of the pass's 64 rows in LDS beside the fp32 tile rows: the
-// tables are stored transposed, [rope_d, M], so each table row t holds the
-// pass's rows as two runs of 32 consecutive floats, loaded as 16-byte vectors.
-constexpr int BIG_RD = 64;                     // the rope form's head width
-constexpr int BIG_SLAB_ROW = 64 + 4;           // floats per slab row (one table column t)
+// The rope forms' head width: the encoder's (rope_d = 64).
+constexpr int BIG_RD = 64;
 
-// The rope form's epilogue. Per pass i (the 64 tile rows of 32-row block i of
-// both wave rows):
-//  1. the pass's rope tables are loaded as 16-byte vectors (table column t,
-//     4 consecutive rows) and the waves write their fp32 blocks to the staging
-//     rows; the tables go to the slab, [cos | sin][t][row];
-//  2. each thread takes one staged row and four 8-feature output chunks (the
-//     lanes of a wave: 16 rows x 4 consecutive chunks, so a row's stores are
-//     64 contiguous bytes). A rope chunk's 8 output features i .. i + 7 of one
-//     half of a head come from computed columns 2i .. 2i + 15 (the
-//     pair-interleaved weight rows) and table columns t = i .. i + 7 (lo half)
-//     or i + D/2 .. (hi half); a chunk past the rope heads is stored plainly.
-// The arithmetic is rope_store4's (each value rounded to fp16, products and
-// sum rounded separately, rounded again), so the result is bit-identical to
-// the other rope epilogues. Host guarantees: rope_d == 64, M % 4 == 0,
-// 16-byte aligned tables, N % 8 == 0, ldc % 8 == 0, 16-byte aligned C, no
-// residual.
-// The tables of pass i as this thread loads them: table tab's column t = idx / 16
-// at 4 consecutive rows (idx % 16) * 4 of the pass's 64, idx = tid + 256 k.
-// Issued before the K loop (they complete ahead of the ring's copies, which
-// are issued after them), so the epilogue never waits on them.
+// The rope forms' epilogue (BM = 128, BN = 128 or 192: two or three heads per
+// tile). Per pass i (the 64 tile rows of 32-row block i of both wave rows) the
+// waves write their fp32 blocks to the staging rows; then each thread takes
+// one staged row and BN / 32 8-feature output chunks (the lanes of a wave: 16
+// rows x 4 consecutive chunks, so a row's stores are 64 contiguous bytes). A
+// rope chunk's 8 output features i .. i + 7 of one half of a head come from
+// computed columns 2i .. 2i + 15 (the pair-interleaved weight rows) and table
+// columns t = i .. i + 7 (lo half) or i + D/2 .. (hi half), which the thread
+// gathered into registers before the K loop (big_rope_tables); a chunk past
+// the rope heads is stored plainly. The arithmetic is rope_store4's (each value
+// rounded to fp16, products and sum rounded separately, rounded again), so the
+// result is bit-identical to the other rope epilogues. Host guarantees:
+// rope_d == 64, N % 8 == 0, ldc % 8 == 0, 16-byte aligned C, no residual.
+// The table values this thread's epilogue uses, gathered before the K loop:
+// in pass i it writes row (wave * 16 + lane % 16) of the pass's 64 and the
+// 8-feature chunks c = lane / 16 + 4 k, whose features sit at
+// f % 64 = 8 (c % 8), that is 8 cq in even k's chunks (the low half of a head,
+// table columns 8 cq .. + 7) and 8 cq + 32 in odd k's (the high half, columns
+// 8 cq + 32 .. + 7). tt[i][half][cos | sin][u]; a row past M reads 0.
 template <int BM, int TM>
-__device__ __forceinline__ void big_rope_tables(const GemmArgs &p, int m0, f32x4 (&tv)[TM][2][4]) {
-    const int tid = threadIdx.x;
+__device__ __forceinline__ void big_rope_tables(const GemmArgs &p, int m0, int wave, int lane,
+                                                float (&tt)[TM][2][2][8]) {
+    const int row = wave * 16 + (lane & 15), cq = lane >> 4;
     const long long ld = p.M;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+        const int m = m0 + (row >> 5) * (BM / 2) + i * 32 + (row & 31);
 #pragma unroll
-        for (int tab = 0; tab < 2; ++tab)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int idx = tid + TPB * k, t = idx >> 4, row4 = (idx & 15) * 4;
-                const int m = m0 + (row4 >> 5) * (BM / 2) + i * 32 + (row4 & 31);
-                const float *src = (tab ? p.rsin : p.rcos) + (long long) t * ld + m;
-                tv[i][tab][k] = m < p.M ? *reinterpret_cast<const f32x4 *>(src) : f32x4{};
-            }
+            for (int tab = 0; tab < 2; ++tab)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    tt[i][h][tab][u] = m < p.M ? (tab ? p.rsin : p.rcos)[(long long) (8 * cq + 32 * h + u) * ld + m]
+                                               : 0.0f;
+    }
 }
 
 template <int ACT, int BM, int BN, int TM, int TN, int EROW>
 __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x16 (&acc)[TN][TM], float *stage,
-                                                  int m0, int n0, int wave, int lane, const f32x4 (&tv)[TM][2][4],
+                                                  int m0, int n0, int wave, int lane, const float (&tt)[TM][2][2][8],
                                                   float bias_own) {
 #pragma clang fp contract(off)
     constexpr int WN = 2, HALF = BIG_RD / 2;
-    float *slab = stage + 64 * EROW;                       // [2][BIG_RD][BIG_SLAB_ROW]
-    float *bias_s = slab + 2 * BIG_RD * BIG_SLAB_ROW;      // [BN], by output feature
+    float *bias_s = stage + 64 * EROW;                     // [BN], by output feature
     const int tid = threadIdx.x, r = lane & 31;
     // bias by output feature, staged once (visible after the first pass's barrier)
     if (tid < BN) bias_s[tid] = bias_own;
     const int row = wave * 16 + (lane & 15);               // this thread's staged row
-    const int cq = lane >> 4;                              // its chunks: cq, cq + 4, cq + 8, cq + 12
+    const int cq = lane >> 4;                              // its chunks: cq, cq + 4, cq + 8, ...
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        // 1. staging writes, slab writes
+        // 1. staging writes
         __builtin_amdgcn_s_barrier();              // the ring's (or the last pass's) reads are done
         const int srow = (wave / WN) * 32 + r;
 #pragma unroll
@@ -1493,13 +1489,6 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
                 *reinterpret_cast<f32x4 *>(stage + srow * EROW + (wave % WN) * (BN / 2) + j * 32 + g * 8 +
                                            (lane >> 5) * 4) =
                     f32x4{acc[j][i][g * 4], acc[j][i][g * 4 + 1], acc[j][i][g * 4 + 2], acc[j][i][g * 4 + 3]};
-#pragma unroll
-        for (int tab = 0; tab < 2; ++tab)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int idx = tid + TPB * k, t = idx >> 4, row4 = (idx & 15) * 4;
-                *reinterpret_cast<f32x4 *>(slab + (tab * BIG_RD + t) * BIG_SLAB_ROW + row4) = tv[i][tab][k];
-            }
         HX_WAIT_LGKM0();
         __builtin_amdgcn_s_barrier();
         // 2. one row, four chunks
@@ -1508,7 +1497,7 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
         f16 *crow = p.C + (long long) m * p.ldc;
         const float *srow_p = stage + row * EROW;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < BN / 32; ++k) {
             const int c = cq + 4 * k, f0 = c * 8, n = n0 + f0;  // output features n .. n + 7
             if (n >= p.N) continue;
             f16x8 o;
@@ -1523,14 +1512,15 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
                     const f32x4 a4 = *reinterpret_cast<const f32x4 *>(src + 4 * q);
                     v[4 * q] = a4[0]; v[4 * q + 1] = a4[1]; v[4 * q + 2] = a4[2]; v[4 * q + 3] = a4[3];
                 }
-                const float *ct = slab + (hi ? lf : i0) * BIG_SLAB_ROW + row;
-                const float *st = ct + BIG_RD * BIG_SLAB_ROW;
+                // table columns lf .. lf + 7: this thread's gathered half k % 2
+                const float(&ct)[8] = tt[i][k & 1][0];
+                const float(&st)[8] = tt[i][k & 1][1];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     // computed column 2 (i0 + u) is feature i0 + u, 2 (i0 + u) + 1 is feature i0 + u + D/2
                     const float x0 = (float) (f16) f32_rounded(act_t<ACT>(v[2 * u] + bias_s[hb + i0 + u]));
                     const float x1 = (float) (f16) f32_rounded(act_t<ACT>(v[2 * u + 1] + bias_s[hb + i0 + u + HALF]));
-                    const float cv = ct[u * BIG_SLAB_ROW], sv = st[u * BIG_SLAB_ROW];
+                    const float cv = ct[u], sv = st[u];
                     if (hi) {
                         const float p1 = x1 * cv, q1 = x0 * sv;
                         o[u] = (f16) f32_rounded(p1 + q1);
@@ -1560,13 +1550,12 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     constexpr int LOADS = (BM + BN) / (8 * NW);    // wave-instructions per ring slice
     constexpr int NR = TM + TN, NM = TM * TN;      // fragment reads and MFMAs per k step
     static_assert(STAGES >= 2 && LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
-    static_assert(!ROPE || (BM == 128 && BN == 128), "the rope form is 128 x 128");
+    static_assert(!ROPE || (BM == 128 && (BN == 128 || BN == 192)), "the rope forms are 128 x 128 and 128 x 192");
     constexpr int EROW = BN + 4;                   // floats per staged row
     constexpr int RING_BYTES = STAGES * (BM + BN) * DS_ROW * 2;
     constexpr int STAGE_BYTES = 64 * EROW * 4;
-    constexpr int SLAB_BYTES = ROPE ? 2 * BIG_RD * BIG_SLAB_ROW * 4 : 0;
     constexpr int BIAS_BYTES = ROPE ? BN * 4 : 0;
-    constexpr int EPI_BYTES = STAGE_BYTES + SLAB_BYTES + BIAS_BYTES;
+    constexpr int EPI_BYTES = STAGE_BYTES + BIAS_BYTES;
     constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
     // one buffer: the A ring, then the B ring; the epilogue reuses all of it
     __shared__ __attribute__((aligned(16))) f16 lds[LDS_BYTES / 2];
@@ -1594,10 +1583,10 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
     }
     // the rope form's tables and bias, loaded now (see big_rope_tables)
-    f32x4 tv[ROPE ? TM : 1][2][4];
+    float tt[ROPE ? TM : 1][2][2][8];
     float bias_own = 0.0f;
     if constexpr (ROPE) {
-        big_rope_tables<BM, TM>(p, m0, tv);
+        big_rope_tables<BM, TM>(p, m0, wave, lane, tt);
         bias_own = (tid < BN && p.bias && n0 + tid < p.N) ? p.bias[n0 + tid] : 0.0f;
     }
     f32x16 acc[TN][TM];
@@ -1681,7 +1670,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         // the activation fixed at compile time: a runtime switch per output
         // would split the unrolled epilogue into a branch per element
         dispatch_epi(p.act, false, [&](auto act_c, auto) {
-            big_rope_epilogue<decltype(act_c)::value, BM, BN, TM, TN, EROW>(p, acc, stage, m0, n0, wave, lane, tv,
+            big_rope_epilogue<decltype(act_c)::value, BM, BN, TM, TN, EROW>(p, acc, stage, m0, n0, wave, lane, tt,
                                                                             bias_own);
         });
         return;
@@ -2022,7 +2011,7 @@ bool launch_big(const GemmArgs &p, Tile t, int stages) {
     HX_BIG(256, 192, 2)
     HX_BIG(128, 256, 2)
     HX_BIG(128, 256, 3)
-    HX_BIG(128, 192, 2)
+    HX_BIG_ROPE(128, 192, 2)
     HX_BIG(128, 192, 3)
     HX_BIG(256, 128, 2)
     HX_BIG(256, 128, 3)
@@ -2041,7 +2030,8 @@ bool launch_big(const GemmArgs &p, Tile t, int stages) {
 // 128 x 128, 8192 x 3072 x 768 46.9 against 49.2, 8192 x 768 x 2304 41.3
 // against 46.0. With the residual epilogue it is slower (8192 x 768 x 768 in
 // the plan: 22.5 us against 19.7; its 24 chunks per row leave 16 threads of
-// each sweep idle), and the rope epilogue exists in the 128 x 128 form: those
+// each sweep idle), and so is the rope epilogue's 128 x 192 form (8192 x 768 x
+// 2304: 53.3 us against 49.8; one workgroup per CU at 302 registers): those
 // take 128 x 128. Both wherever the grid fills at least one round of 256
 // workgroups; with fewer tiles (784 rows, 2048 x 3072 x 1024) the other paths
 // are faster.
@@ -2232,15 +2222,13 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
     const bool kw_ok = MODE == B_NK && batch == 1 && p.K % KW_BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                        avec && bvec && (p.M + 31) / 32 <= 65535 && !p.ln_w;
     // the large-tile kernel: its epilogue stores 8-column chunks (and, with the
-    // rope, stages 64-wide heads' tables as 16-byte vectors of 4 rows: rope_d
-    // 64, M % 4 == 0, 16-byte aligned tables, whole 8-column chunks of rope
-    // columns, no residual)
+    // rope, takes 64-wide heads in whole 8-column chunks of rope columns, no
+    // residual)
     const bool big_ok = MODE == B_NK && batch == 1 && p.K % BK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
                         avec && bvec && !p.ln_w && p.N % 8 == 0 && p.ldc % 8 == 0 &&
                         ((uintptr_t) p.C & 15) == 0 && (!p.bias || ((uintptr_t) p.bias & 15) == 0) &&
                         (!p.R || (p.ldr % 8 == 0 && ((uintptr_t) p.R & 15) == 0)) &&
-                        (!p.rcos || (p.rope_d == BIG_RD && p.rope_cols % 8 == 0 && !p.R && p.M % 4 == 0 &&
-                                     ((uintptr_t) p.rcos & 15) == 0 && ((uintptr_t) p.rsin & 15) == 0));
+                        (!p.rcos || (p.rope_d == BIG_RD && p.rope_cols % 8 == 0 && !p.R));
     if (big_ok && (path == 5 || path == 0)) {
         const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N, !p.rcos && !p.R);
         const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;

@@ -614,9 +614,8 @@ def test_big_tile_rope_epilogue(dev, form, M, Kd, heads, d, extra, act):
     automatic choice where the grid fills a round: form None) is bit-identical
     to the same kernel's plain output followed by rope_2d on the q and k
     heads; ragged M, head widths 16 to 64, every activation. Its 128 x 128
-    form stages each pass's tables in LDS (rope_d 64, M % 4 == 0); the other
-    cases (M = 1102, narrower heads, the 128 x 192 tile) take the other rope
-    epilogues."""
+    and 128 x 192 forms take rope_d 64 (each thread gathering its own table
+    values); narrower heads take the other rope epilogues."""
     r = rng(23)
     N = 2 * heads * d + extra
     a = h16(r.standard_normal((M, Kd)))
