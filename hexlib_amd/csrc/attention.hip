@@ -376,7 +376,10 @@ __global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ 
     constexpr int PIECES = KS_KEYS * VCH / (64 * QG);          // 16-byte pieces per lane per tensor
     static_assert(KS_KEYS * VCH % (64 * QG) == 0, "the stage splits evenly over the split's waves");
     constexpr int PO_STRIDE = D + 4;
-    constexpr int RING_BYTES = KS * 2 * SLOT * 2;
+    // two ring slots per split, one with four splits (their LDS would not fit
+    // twice; at 256 tokens each split then has one stage anyway)
+    constexpr int SLOTS = KS >= 4 ? 1 : 2;
+    constexpr int RING_BYTES = KS * SLOTS * SLOT * 2;
     constexpr int MERGE_BYTES = KS > 1 ? W * 32 * PO_STRIDE * 4 : 0;
     constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
     __shared__ __attribute__((aligned(16))) f16 ring[LDS_BYTES / 2];
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ 
         }
     };
     auto store_stage = [&](int slot) {
-        f16 *kt = ring + (ks * 2 + slot) * SLOT, *vt = kt + K_HALVES;
+        f16 *kt = ring + (ks * SLOTS + slot) * SLOT, *vt = kt + K_HALVES;
 #pragma unroll
         for (int i = 0; i < PIECES; ++i) {
             const int e = qg * 64 + lane + 64 * QG * i, key = e / VCH, ch = e % VCH;
@@ -443,11 +446,11 @@ __global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ 
     store_stage(0);
     __syncthreads();
     for (int it = 0; it < iters; ++it) {
-        const int st = it * KS + ks, slot = it & 1;
+        const int st = it * KS + ks, slot = SLOTS == 2 ? it & 1 : 0;
         const bool live = st < n_stages;
         if (live && st + KS < n_stages) load_stage(st + KS);   // one stage ahead, into registers
         if (live) {
-            const f16 *kt = ring + (ks * 2 + slot) * SLOT, *vt = kt + K_HALVES;
+            const f16 *kt = ring + (ks * SLOTS + slot) * SLOT, *vt = kt + K_HALVES;
             const int key0 = st * KS_KEYS;
             f32x16 s[2];
 #pragma unroll
@@ -481,9 +484,11 @@ __global__ __launch_bounds__(64 * QG * KS) void attn_qg(const f16 *__restrict__ 
                     }
         }
         // the other slot was last read in the previous iteration: every wave is
-        // past it once this barrier is, so the next stage can land there
+        // past it once this barrier is, so the next stage can land there (one
+        // slot: every wave must be past this stage's reads first)
         if (it + 1 < iters) {
-            if (live && st + KS < n_stages) store_stage(slot ^ 1);
+            if constexpr (SLOTS == 1) __syncthreads();
+            if (live && st + KS < n_stages) store_stage(SLOTS == 2 ? slot ^ 1 : 0);
             __syncthreads();
         }
     }
@@ -568,6 +573,7 @@ bool launch_qg(int qg, int ks, const f16 *Q, const f16 *K, long long ldqk, const
     HX_QG(64, 2, 1)
     HX_QG(64, 2, 2)
     HX_QG(64, 4, 2)
+    HX_QG(64, 1, 4)
     HX_QG(32, 4, 1)
     HX_QG(32, 2, 2)
 #undef HX_QG
@@ -582,6 +588,9 @@ bool launch_qg(int qg, int ks, const f16 *Q, const f16 *K, long long ldqk, const
 int qg_auto(int T, int H, int batch) {
     const long long heads = (long long) batch * H;
     if (heads * ((T + 127) / 128) >= 2 * CUS) return 41;
+    // one image of up to 256 tokens (12 heads: 96 workgroups): four key splits
+    // of one 32-query group, each split one stage (4.83 us against 5.07)
+    if (T <= 256 && heads * ((T + 31) / 32) <= CUS / 2) return 14;
     // a few images (batch 4: 48 heads): two key splits of two query groups
     // share each stage (5.8 us against 6.5)
     if (T <= 512 && heads * ((T + 63) / 64) >= CUS / 2) return 22;
@@ -622,7 +631,7 @@ bool dims_ok(int rows, int H, int D, int batch) {
 }  // namespace
 
 extern "C" int hexlib_gpu_attention_override(int form) {
-    const bool ok = form == 0 || form == 1 || form == 41 || form == 21 || form == 22 || form == 42;
+    const bool ok = form == 0 || form == 1 || form == 41 || form == 21 || form == 22 || form == 42 || form == 14;
     if (!ok) return HEXLIB_DSP_ERR_INVAL_PARAMS;
     g_attn_form = form;
     return HEXLIB_DSP_OK;

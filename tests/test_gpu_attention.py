@@ -131,15 +131,17 @@ def test_attention_qkv(dev, B, T, H, D):
     assert K.close_f16(got, want, 1e-2, 1e-3).all()
 
 
-@pytest.mark.parametrize("form", [41, 21, 22, 42, 1])
+@pytest.mark.parametrize("form", [41, 21, 22, 42, 14, 1])
 @pytest.mark.parametrize("B,T,H,D", [(4, 256, 2, 64), (1, 784, 2, 64), (2, 100, 3, 64), (3, 33, 2, 32),
                                      (1, 1, 1, 64), (2, 130, 2, 32)])
 def test_attention_forms(dev, form, B, T, H, D):
     """Every attention form, forced through the override: the shared-K/V
     kernel with QG query groups and KS key splits (form QG * 10 + KS; the
-    D = 32 build has 41 and 22, other forms fall back), and the per-wave-tiles
-    kernel (1). Ragged T leaves partial query groups, partial 64-key stages
-    and key splits with no stage at all; each against the float64 oracle."""
+    D = 32 build has 41 and 22, other forms fall back; 14 has one ring slot
+    per split, so 784 tokens reuse it stage after stage), and the
+    per-wave-tiles kernel (1). Ragged T leaves partial query groups, partial
+    64-key stages and key splits with no stage at all; each against the
+    float64 oracle."""
     r = np.random.default_rng(100 + T + form)
     q, k, v = (h16(r.standard_normal((B * T, H, D))) for _ in range(3))
     assert dev.lib.hexlib_gpu_attention_override(form) == 1
@@ -153,6 +155,6 @@ def test_attention_forms(dev, form, B, T, H, D):
 
 
 def test_attention_override_rejects_unknown_forms(dev):
-    for form in (2, 3, 11, 14, 44, -1):
+    for form in (2, 3, 11, 12, 44, -1):
         assert dev.lib.hexlib_gpu_attention_override(form) != 1
     assert dev.lib.hexlib_gpu_attention_override(0) == 1
