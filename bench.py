@@ -201,10 +201,13 @@ def dominant_op(g, wb):
     return {"spec": spec, "index": -neg_idx, "count": count, "inputs": ins, "output": out}
 
 
-def roofline(plan, g, reps: int = 200, iters: int = 7) -> dict:
+def roofline(plan, g, reps: int = 200, iters: int = 7, cold: bool = True) -> dict:
     """Algorithmic work of one launch of the dominant op / its mean duration,
     measured with HIP events on the session stream around a captured graph of
-    `reps` back-to-back launches (cycles_total of a TIMED invoke / reps)."""
+    `reps` back-to-back launches (cycles_total of a TIMED invoke / reps).
+    With `cold`, also the same linear over a >= 512 MiB operand rotation
+    (`roofline_cold`); --roofline-only leaves it out, so that its rocprofv3
+    trace holds the warm launches only."""
     d = dominant_op(g, plan.batch)
     shapes = [s for s, _ in d["inputs"]]
     dtypes = [t for _, t in d["inputs"]]
@@ -230,7 +233,7 @@ def roofline(plan, g, reps: int = 200, iters: int = 7) -> dict:
     out["traffic"] = measured_traffic(out["kernel"])
     out["cache"] = (f"warm: {reps} back-to-back launches on the plan's own operands, which stay in "
                     f"L2 / the 256 MB last-level cache; 'cold' below rotates >= 512 MiB of distinct operands")
-    if d["spec"] == "matmul_epilogue_f16wt":
+    if cold and d["spec"] == "matmul_epilogue_f16wt":
         out["cold"] = roofline_cold(plan.session, m, k, n, nbytes, flops, out["bound"])
     return out
 
@@ -869,7 +872,7 @@ def main() -> int:
     if args.roofline_only:
         if args.copy_ref:
             copy_reference()
-        roof = roofline(plan, g)
+        roof = roofline(plan, g, cold=False)
         plan.close()
         session.close()
         print(json.dumps({"roofline": roof}))
