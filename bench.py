@@ -939,8 +939,9 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: seeded U[0,1] image, N(0,0.02) fp16 weights, random init",
         "config": {"workload": "vit_encoder_256_b1 (BASELINE cfg 4: 12 blocks, hidden 768, "
-                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; per block one q/k/v linear, "
-                               f"one q/k rope op, one fused attention op; {wb.n_ops} ops as one hipGraph)",
+                               "12 heads, MLP 3072, LayerNorm, 2D RoPE, merger; per block one q/k/v linear "
+                               "with the q/k rope in its epilogue, one fused attention op, the residual adds "
+                               f"in the linears' epilogues; {wb.n_ops} ops as one hipGraph)",
                    "image": 256, "batch": 1, "tokens": 256, "attention": cfg.attention,
                    "plan_ops": wb.n_ops, "plan_gpu_ns": plan_gpu_ns},
         "roofline": roof,

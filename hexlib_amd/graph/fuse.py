@@ -103,8 +103,13 @@ def fuse_residual(graph: Graph) -> Graph:
         other = [n for n in add.inputs if n != out]
         if len(add.inputs) != 2 or len(other) != 1:
             continue
+        # the other addend may be an activation of the output's dtype or a
+        # stored table of the output's shape (the encoder's fp32 position
+        # embedding, staged in the add's fp16 either way)
         res = graph.tensor(other[0])
-        if res.const or res.shape != graph.tensor(out).shape or res.dtype != graph.tensor(out).dtype:
+        if res.shape != graph.tensor(out).shape:
+            continue
+        if res.dtype != graph.tensor(out).dtype and not (res.const and res.dtype == "fp32"):
             continue
         replaced[op.id] = Op(id=op.id, kind="matmul_epilogue",
                              inputs=op.inputs + (other[0],), outputs=add.outputs,

@@ -267,7 +267,7 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     fused_feeds = E.fuse_qkv_feeds(feeds, cfg) if mode == "fused_qkv_rope" else feeds
     (out,), wb = _run_plan(session, cfg, fused_feeds, graph_mode=True, residual=residual, rope=rope,
                            layernorm=ln, weight_layout="auto" if residual or rope or ln else None)
-    assert wb.n_ops == (259 - 12 * (8 if mode == "fused" else 11) - (24 if residual else 0)
+    assert wb.n_ops == (259 - 12 * (8 if mode == "fused" else 11) - (25 if residual else 0)
                         - (12 if rope else 0) - (12 if ln else 0))
     want = _oracle(cfg_ref, feeds)
     err = np.abs(out - want).max()
@@ -308,7 +308,7 @@ def test_product_plan_at_batch_32(session):
     cfg = replace(cfg_ref, attention="fused_qkv_rope")
     (out,), wb = _run_plan(session, cfg, E.fuse_qkv_feeds(feeds, cfg), graph_mode=True, residual=True,
                            rope=True, weight_layout="auto")
-    assert wb.n_ops == 259 - 12 * 11 - 24 - 12
+    assert wb.n_ops == 259 - 12 * 11 - 25 - 12
     per = out.shape[0] // 32
     for i in (0, 17, 31):
         want = _oracle(cfg1, _image_feeds(cfg1, feeds, i))

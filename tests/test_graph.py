@@ -207,9 +207,10 @@ def test_fused_qkv_feeds_compute_the_reference_function():
 
 
 def test_fuse_residual():
-    """Each block's two residual adds fold into the fp16 linear feeding them;
-    the pos_embed add (const operand) and q4_0 linears do not; on the
-    storage-rounding oracle the result is unchanged bit for bit."""
+    """Each block's two residual adds fold into the fp16 linear feeding them,
+    and so does the pos_embed add (a stored table of the output's shape) into
+    the patch-embed linear; q4_0 linears do not; on the storage-rounding
+    oracle the result is unchanged bit for bit."""
     from dataclasses import replace as _replace
     from hexlib_amd.graph.fuse import fuse_residual
     from oracle import eager
@@ -217,9 +218,9 @@ def test_fuse_residual():
     g = E.build_vision_encoder(cfg)
     f = fuse(g)
     r = fuse_residual(f)
-    assert len(f.ops) - len(r.ops) == 2 * cfg.depth
-    assert sum(1 for o in r.ops if o.kind == "matmul_epilogue" and len(o.inputs) == 4) == 2 * cfg.depth
-    assert sum(1 for o in r.ops if o.kind == "add") == 1
+    assert len(f.ops) - len(r.ops) == 2 * cfg.depth + 1
+    assert sum(1 for o in r.ops if o.kind == "matmul_epilogue" and len(o.inputs) == 4) == 2 * cfg.depth + 1
+    assert sum(1 for o in r.ops if o.kind == "add") == 0
     feeds = E.synthetic_feeds(g, cfg, seed=5)
     a = eager.run_stored(f, feeds)[g.outputs[0]]
     b = eager.run_stored(r, feeds)[g.outputs[0]]
@@ -229,8 +230,8 @@ def test_fuse_residual():
     cfgq = _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
     gq = E.build_vision_encoder(cfgq)
     wb = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), residual=True)
-    assert wb.n_ops == 259 - 12 * 11 - 24
-    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_f16wt_res") == 24
+    assert wb.n_ops == 259 - 12 * 11 - 25
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_f16wt_res") == 25
 
 
 def test_fuse_rope():
@@ -260,7 +261,7 @@ def test_fuse_rope():
     cfgq = _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
     gq = E.build_vision_encoder(cfgq)
     wb = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), residual=True, rope=True)
-    assert wb.n_ops == 259 - 12 * 11 - 24 - 12
+    assert wb.n_ops == 259 - 12 * 11 - 25 - 12
     assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_f16wt_rope") == 12
     assert sum(1 for s in wb.op_specs if s == "attention_qkv") == 12
     assert KIND_ID_OF("matmul_epilogue_f16wt_rope") == 22 and KIND_ID_OF("attention_qkv") == 23
@@ -300,7 +301,7 @@ def test_fuse_layernorm():
     q4 = fuse(E.build_vision_encoder(_replace(E.QWEN35_VISION_FP16, weight_dtype="q4_0")))
     assert fuse_layernorm(q4) is q4
     wb = WP.build_whole_plan_batch(g, E.synthetic_feeds(g, cfg), residual=True, rope=True, layernorm=True)
-    assert wb.n_ops == 259 - 12 * 11 - 24 - 12 - 12
+    assert wb.n_ops == 259 - 12 * 11 - 25 - 12 - 12
     assert sum(1 for s in wb.op_specs if s == "layernorm_matmul_epilogue_f16wt") == 12
     assert KIND_ID_OF("layernorm_matmul_epilogue_f16wt") == 24
 
