@@ -1435,12 +1435,12 @@ constexpr int BIG_RD = 64;
 // rope chunk's 8 output features i .. i + 7 of one half of a head come from
 // computed columns 2i .. 2i + 15 (the pair-interleaved weight rows) and table
 // columns t = i .. i + 7 (lo half) or i + D/2 .. (hi half), which the thread
-// gathered into registers before the K loop (big_rope_tables); a chunk past
+// gathers into registers when the K loop is done (big_rope_tables); a chunk past
 // the rope heads is stored plainly. The arithmetic is rope_store4's (each value
 // rounded to fp16, products and sum rounded separately, rounded again), so the
 // result is bit-identical to the other rope epilogues. Host guarantees:
 // rope_d == 64, N % 8 == 0, ldc % 8 == 0, 16-byte aligned C, no residual.
-// The table values this thread's epilogue uses, gathered before the K loop:
+// The table values this thread's epilogue uses, gathered after the K loop:
 // in pass i it writes row (wave * 16 + lane % 16) of the pass's 64 and the
 // 8-feature chunks c = lane / 16 + 4 k, whose features sit at
 // f % 64 = 8 (c % 8), that is 8 cq in even k's chunks (the low half of a head,
@@ -1582,13 +1582,9 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         b0 = *reinterpret_cast<const f32x4 *>(p.bias + n);
         b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
     }
-    // the rope form's tables and bias, loaded now (see big_rope_tables)
-    float tt[ROPE ? TM : 1][2][2][8];
+    // the rope form's bias, loaded now
     float bias_own = 0.0f;
-    if constexpr (ROPE) {
-        big_rope_tables<BM, TM>(p, m0, wave, lane, tt);
-        bias_own = (tid < BN && p.bias && n0 + tid < p.N) ? p.bias[n0 + tid] : 0.0f;
-    }
+    if constexpr (ROPE) bias_own = (tid < BN && p.bias && n0 + tid < p.N) ? p.bias[n0 + tid] : 0.0f;
     f32x16 acc[TN][TM];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -1667,6 +1663,12 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     HX_WAIT_VMCNT(0);
     f16 *C = p.C;
     if constexpr (ROPE) {
+        // The tables are gathered here, after the K loop, where the fragment
+        // registers are free: held through the loop they raised the 128 x 192
+        // form to 302 registers, one workgroup per CU. Their latency runs
+        // under the first pass's staging writes.
+        float tt[TM][2][2][8];
+        big_rope_tables<BM, TM>(p, m0, wave, lane, tt);
         // the activation fixed at compile time: a runtime switch per output
         // would split the unrolled epilogue into a branch per element
         dispatch_epi(p.act, false, [&](auto act_c, auto) {
@@ -2030,14 +2032,16 @@ bool launch_big(const GemmArgs &p, Tile t, int stages) {
 // 128 x 128, 8192 x 3072 x 768 46.9 against 49.2, 8192 x 768 x 2304 41.3
 // against 46.0. With the residual epilogue it is slower (8192 x 768 x 768 in
 // the plan: 22.5 us against 19.7; its 24 chunks per row leave 16 threads of
-// each sweep idle), and so is the rope epilogue's 128 x 192 form (8192 x 768 x
-// 2304: 53.3 us against 49.8; one workgroup per CU at 302 registers): those
-// take 128 x 128. Both wherever the grid fills at least one round of 256
-// workgroups; with fewer tiles (784 rows, 2048 x 3072 x 1024) the other paths
-// are faster.
-Tile big_auto(int M, int N, bool plain) {
+// each sweep idle), so that form takes 128 x 128. The rope epilogue takes
+// 128 x 192 since its table gather moved after the K loop (236 registers, two
+// workgroups per CU; gathered before the loop it needed 302, one workgroup per
+// CU, and lost to 128 x 128): the q/k/v + rope linear 40.8 us against 45.3,
+// the batch-32 plan 2.66 ms against 2.72. Both wherever the grid fills at
+// least one round of 256 workgroups; with fewer tiles (784 rows, 2048 x 3072 x
+// 1024) the other paths are faster.
+Tile big_auto(int M, int N, bool no_residual) {
     const long long t192 = (long long) ((M + 127) / 128) * ((N + 191) / 192);
-    if (plain && N % 192 == 0 && t192 >= 256) return Tile{128, 192};
+    if (no_residual && N % 192 == 0 && t192 >= 256) return Tile{128, 192};
     const long long tiles = (long long) ((M + 127) / 128) * ((N + 127) / 128);
     return tiles >= 256 ? Tile{128, 128} : Tile{0, 0};
 }
@@ -2230,7 +2234,7 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
                         (!p.R || (p.ldr % 8 == 0 && ((uintptr_t) p.R & 15) == 0)) &&
                         (!p.rcos || (p.rope_d == BIG_RD && p.rope_cols % 8 == 0 && !p.R));
     if (big_ok && (path == 5 || path == 0)) {
-        const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N, !p.rcos && !p.R);
+        const Tile bt = path == 5 ? Tile{g_ov_bm.load(), g_ov_bn.load()} : big_auto(p.M, p.N, !p.R);
         const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;
         if (bt.bm && launch_big(p, bt, stages)) return;
     }
