@@ -66,7 +66,7 @@ def op_work(spec_name: str, in_shapes, out_shape, in_dtypes, out_dtype) -> tuple
         rows, h, d = in_shapes[0][0], in_shapes[0][-2], in_shapes[0][-1]
         t = rows // max(1, _ATTN_BATCH.get(tuple(in_shapes[0]), 1))
         return "mfma", 4.0 * rows * t * h * d
-    if spec_name.startswith("matmul_epilogue"):
+    if spec_name.startswith(("matmul_epilogue", "lnfold_matmul_epilogue")):   # (x, W, bias ...)
         m, k = in_shapes[0]
         n = in_shapes[1][-1]
         return "mfma", 2.0 * m * k * n
@@ -87,11 +87,18 @@ def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
 
 # ---- plan helpers -------------------------------------------------------------------------
 
-def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True, layernorm=False):
+FOLD_LN_ROWS = 256
+
+
+def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True, layernorm=False,
+               fold_ln_rows=None):
     """The product plan: fusions on (`residual` folds residual adds into the
     fp16 linears, `rope` the q/k rope into the fused q/k/v linear; the
-    config's `attention` picks the attention form). `layernorm` (folding a
-    LayerNorm into the linear it feeds) is off: every workgroup of that
+    config's `attention` picks the attention form). Each LayerNorm of at most
+    `fold_ln_rows` rows (default FOLD_LN_ROWS: the batch-1 256x256 plan) is
+    folded algebraically into the linear it feeds (`fold_layernorm`: no
+    launch of its own). `layernorm` (the normalised rows recomputed in the
+    linear's prologue) is off: every workgroup of that
     kernel normalises its whole row block again, 48 times per row at fc1,
     which costs more than the separate launch it saves (18.6 us against
     9.4 + 2.5 us on MI355X; a K-across-waves form with the row block resident
@@ -101,10 +108,12 @@ def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True, laye
     from hexlib_amd.exec.wholeplan import build_whole_plan_batch
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=seed)
+    fold = FOLD_LN_ROWS if fold_ln_rows is None else fold_ln_rows
     return g, feeds, build_whole_plan_batch(g, feeds, weight_layout=weight_layout,
                                             residual=residual and cfg.attention != "unfused",
                                             rope=rope and cfg.attention == "fused_qkv_rope",
-                                            layernorm=layernorm and cfg.attention != "unfused")
+                                            layernorm=layernorm and cfg.attention != "unfused",
+                                            fold_ln_rows=fold if cfg.attention != "unfused" else 0)
 
 
 def time_replays(plan, steps: int, warmup: int) -> float:
@@ -189,11 +198,10 @@ def dominant_op(g, wb):
     """The plan's GEMM row with the most algorithmic work per image (launches
     x FLOPs; ties: first in plan order). For the cfg-4 encoder plan that is
     the MLP up-projection fc1, 256x768x3072 with its LayerNorm folded in (12
-    launches, tied with fc2 in work; fc1 runs as one kernel, fc2 as split-K
-    partials plus a reduction)."""
+    launches, tied with fc2 in work and first in plan order)."""
     rows = []
     for (spec, ins, out), (count, idx, _) in unique_ops(g, wb).items():
-        if not spec.startswith(("matmul_epilogue", "layernorm_matmul_epilogue")):
+        if not spec.startswith(("matmul_epilogue", "layernorm_matmul_epilogue", "lnfold_matmul_epilogue")):
             continue
         flops = op_work(spec, [s for s, _ in ins], out[0], [d for _, d in ins], out[1])[1]
         rows.append((count * flops, -idx, spec, ins, out, count))
@@ -233,13 +241,14 @@ def roofline(plan, g, reps: int = 200, iters: int = 7, cold: bool = True) -> dic
     out["traffic"] = measured_traffic(out["kernel"])
     out["cache"] = (f"warm: {reps} back-to-back launches on the plan's own operands, which stay in "
                     f"L2 / the 256 MB last-level cache; 'cold' below rotates >= 512 MiB of distinct operands")
-    if cold and d["spec"] == "matmul_epilogue_f16wt":
-        out["cold"] = roofline_cold(plan.session, m, k, n, nbytes, flops, out["bound"])
+    if cold and d["spec"] in ("matmul_epilogue_f16wt", "lnfold_matmul_epilogue_f16wt"):
+        out["cold"] = roofline_cold(plan.session, m, k, n, nbytes, flops, out["bound"],
+                                    lnfold=d["spec"].startswith("lnfold"))
     return out
 
 
 def roofline_cold(session, M: int, K: int, N: int, nbytes: int, flops: int, bound: str,
-                  rotation_mib: int = 512) -> dict:
+                  rotation_mib: int = 512, lnfold: bool = False) -> dict:
     """The dominant W^T linear (gelu epilogue, as fc1) over enough distinct
     (A, W^T, bias, out) sets that one pass touches >= rotation_mib MiB, more
     than the 256 MB last-level cache: each launch then reads its operands from
@@ -250,27 +259,34 @@ def roofline_cold(session, M: int, K: int, N: int, nbytes: int, flops: int, boun
     from hexlib_amd import lib as L
     lib = L.load()
     P = ctypes.c_void_p
-    per_set = (M * K + N * K + M * N) * 2 + N * 4
+    nb = 2 * N if lnfold else N   # the folded LayerNorm's bias2 = [c2 | c1]
+    per_set = (M * K + N * K + M * N) * 2 + nb * 4
     nsets = -(-(rotation_mib << 20) // per_set)
     gen = torch.Generator(device="cuda").manual_seed(11)
     sets = [(torch.randn(M, K, device="cuda", generator=gen).half(),
              (torch.randn(N, K, device="cuda", generator=gen) * 0.02).half(),
-             torch.randn(N, device="cuda", generator=gen) * 0.02,
+             torch.randn(nb, device="cuda", generator=gen) * 0.02,
              torch.empty(M, N, device="cuda", dtype=torch.float16)) for _ in range(nsets)]
+
+    def launch(a, w, b, o):
+        if lnfold:
+            lib.lnfold_matmul_epilogue_f16wt_fp16(P(a.data_ptr()), P(w.data_ptr()), P(b.data_ptr()),
+                                                  P(o.data_ptr()), M, K, N, 1, ctypes.c_float(1e-6))
+        else:
+            lib.matmul_epilogue_f16wt_fp16(P(a.data_ptr()), P(w.data_ptr()), P(b.data_ptr()), P(o.data_ptr()),
+                                           M, K, N, 1)
     stream = torch.cuda.Stream()
     saved = lib.hexlib_gpu_get_stream()
     try:
         with torch.cuda.stream(stream):
             lib.hexlib_gpu_set_stream(P(stream.cuda_stream))
             for a, w, b, o in sets[:2]:   # warm the code path outside the capture
-                lib.matmul_epilogue_f16wt_fp16(P(a.data_ptr()), P(w.data_ptr()), P(b.data_ptr()), P(o.data_ptr()),
-                                               M, K, N, 1)
+                launch(a, w, b, o)
             stream.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
                 for a, w, b, o in sets:
-                    lib.matmul_epilogue_f16wt_fp16(P(a.data_ptr()), P(w.data_ptr()), P(b.data_ptr()),
-                                                   P(o.data_ptr()), M, K, N, 1)
+                    launch(a, w, b, o)
             graph.replay()
             stream.synchronize()
             best = float("inf")
@@ -805,6 +821,7 @@ def run_variant(session, vcfg, steps: int, label: str) -> dict:
 # ---- main -------------------------------------------------------------------------------
 
 def main() -> int:
+    global FOLD_LN_ROWS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -820,6 +837,9 @@ def main() -> int:
                     help="time the four batch-32 product linears in the plan and torch.matmul on the "
                          "same shapes, print them and exit (the rocprofv3 --pmc target for those GEMMs)")
     ap.add_argument("--no-library", action="store_true", help="with --gemm-b32: skip torch.matmul")
+    ap.add_argument("--fold-ln-rows", type=int, default=None,
+                    help="fold LayerNorms of at most this many rows into their linear (default "
+                         f"{FOLD_LN_ROWS}; 0: every LayerNorm its own launch)")
     ap.add_argument("--plan-only", metavar="VARIANT",
                     choices=("256_b1", "256_b32", "448_b1", "256_b1_q8_0", "256_b1_q4_0"),
                     help="build that plan, time --steps graph replays of it and exit (a rocprofv3 "
@@ -829,6 +849,8 @@ def main() -> int:
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 output directory and exit")
     args = ap.parse_args()
+    if args.fold_ln_rows is not None:
+        FOLD_LN_ROWS = args.fold_ln_rows
     if args.trace_summary:
         print(trace_summary(args.trace_summary))
         return 0

@@ -76,6 +76,10 @@ struct GemmArgs {
     // out = epilogue(LN(A) @ B), LN(A) rounded to fp16 as layernorm_fp16 stores it
     const float *ln_w, *ln_b;
     float ln_eps;
+    // folded LayerNorm (gemm_nk_kw<..., LNF>): A is the LayerNorm's raw input x,
+    // B its weight-scaled W'^T, and bias holds 2N floats, c2 then c1 (see
+    // gemm_nk_kw); the row statistics are taken from the A tiles in the ring
+    float lnf_eps;
 };
 
 __device__ __forceinline__ bool hx_aligned8(const void *p) {
@@ -1136,6 +1140,28 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
     else rope_block_store<0>(p, m, nb, lane, v, rb);
 }
 
+// The folded LayerNorm's c1 (bias[N + n]) for the lane's 16 accumulator
+// columns of the 32-column block at nb: column nb + 8 g + 4 (lane / 32) + e,
+// or, for a rope head's pair-interleaved columns, the output feature that
+// column holds (the bias's own index, as rope_block_load takes it).
+__device__ __forceinline__ void load_block_c1(const GemmArgs &p, int nb, int lane, float (&c1)[16]) {
+    const float *src = p.bias + p.N;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + (lane >> 5) * 4;
+        int f[4] = {n, n + 1, n + 2, n + 3};
+        if (p.rcos && n < p.rope_cols) {
+            const RopeQuad q = rope_quad(n, p.rope_d);
+            f[0] = q.lo;
+            f[1] = q.hi;
+            f[2] = q.lo + 1;
+            f[3] = q.hi + 1;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c1[g * 4 + e] = n + e < p.N ? src[f[e]] : 0.0f;
+    }
+}
+
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
 // 2 stages -- 128 KB of LDS). With T = 64 wave w stores block w after the
 // reduction; with T = 32 wave 0 stores.
@@ -1147,11 +1173,21 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
 // loaded into registers while the previous stage is multiplied, then
 // dequantized (fp16(d * q), fp16(d * (q - 8))) into the same LDS layout the
 // fp16 copies fill.
-template <int T, bool ROPE = false, bool KN = false, int QB = 0>
+// LNF: a LayerNorm over A's rows (all K) folded into the product. With
+// W'[n][k] = fp16(ln_w[k] W[n][k]), c1[n] = sum_k W'[n][k] and
+// c2[n] = bias[n] + sum_k ln_b[k] W[n][k] (prepared on the host),
+//   LN(x) W^T + bias = rstd (x W'^T - mean c1) + c2,
+// so the ring multiplies the raw x, and each wave also sums x and x^2 over the
+// fragments it reads (v_dot2_f32_f16: two halves per instruction, products
+// exact in fp32). The four waves' sums give the row's mean and one-pass
+// variance in fp32 after the loop; the epilogue applies
+// rstd (acc - mean c1[n]) before the bias (c2) and the activation.
+template <int T, bool ROPE = false, bool KN = false, int QB = 0, bool LNF = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
     static_assert(QB == 0 || (!ROPE && (QB == 8 || QB == 4) && (!KN || QB == 4)),
                   "quantized weights: q8_0 / q4_0 blocks along K of W^T, or q4_0 blocks along N of [K][N]");
+    static_assert(!LNF || (T == 64 && !KN && QB == 0), "the folded LayerNorm takes the 64x64 W^T form");
     constexpr bool Q8 = QB != 0;                 // a block-quantized weight (either format)
     constexpr int QBYTES = QB == 8 ? 34 : 18;
     constexpr int NB = T / 32;                 // 32-row blocks per tile side
@@ -1245,6 +1281,11 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         if (wave < NB * NB)
             rblk = load_block_rope(p, m0 + (wave / NB) * 32 + (lane & 31), n0 + (wave % NB) * 32, lane);
     }
+    // LNF: c1 of the lane's 16 output columns (bias + N, indexed as the bias is)
+    float lc1[16] = {};
+    if constexpr (LNF) {
+        if (wave < NB * NB) load_block_c1(p, n0 + (wave % NB) * 32, lane, lc1);
+    }
     if constexpr (!ROPE) {
         bbias = load_block_bias(p, n0 + (wave % NB) * 32);
         if (p.R && wave < NB * NB) {
@@ -1269,6 +1310,9 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     for (int s = 0; s < (FULL ? STAGES : STAGES - 1); ++s)
         if (s < KT) issue(s, s);
     const int r = lane & 31;
+    // LNF: this lane's sums of x and x^2 over the A fragments it reads (row
+    // h * 32 + r, the k chunks of parity lane / 32 of this wave's sub-slices)
+    float xs[NB] = {}, xq[NB] = {};
     auto mma_stage = [&](int st) {
         const f16 *as = sA[st][wave], *bs = sB[st][wave];
 #pragma unroll
@@ -1286,6 +1330,17 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             for (int j = 0; j < NB; ++j)
 #pragma unroll
                 for (int i = 0; i < NB; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+            if constexpr (LNF) {
+                const f16x2 one2 = {(f16) 1.0f, (f16) 1.0f};
+#pragma unroll
+                for (int h = 0; h < NB; ++h)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f16x2 pr = {xf[h][2 * u], xf[h][2 * u + 1]};
+                        xs[h] = __builtin_amdgcn_fdot2(pr, one2, xs[h], false);
+                        xq[h] = __builtin_amdgcn_fdot2(pr, pr, xq[h], false);
+                    }
+            }
         }
     };
     if constexpr (Q8) {
@@ -1370,6 +1425,13 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             for (int e4 = 0; e4 < 4; ++e4)
                 *reinterpret_cast<f32x4 *>(red + (((wave * NB * NB + i * NB + j) * 4 + e4) * 64 + lane) * 4) =
                     f32x4{acc[j][i][4 * e4], acc[j][i][4 * e4 + 1], acc[j][i][4 * e4 + 2], acc[j][i][4 * e4 + 3]};
+    // LNF: each lane's (sum x, sum x^2) pairs, [wave][row block][lane], in the
+    // drained B ring (the partial tiles fill the A ring)
+    float2 *lst = reinterpret_cast<float2 *>(&sB[0][0][0]);
+    if constexpr (LNF) {
+#pragma unroll
+        for (int h = 0; h < NB; ++h) lst[(wave * NB + h) * 64 + lane] = float2{xs[h], xq[h]};
+    }
     HX_WAIT_LGKM0();
     __builtin_amdgcn_s_barrier();
     if (wave >= NB * NB) return;
@@ -1385,6 +1447,23 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         }
     // lane l holds output row l % 32 of the block, columns 8 g + 4 (l / 32) .. + 3
     const int m = m0 + (blk / NB) * 32 + r;
+    if constexpr (LNF) {
+        // the row's sums, in a fixed order (wave 0..3, then the two lanes of the row)
+        float sx = 0.0f, sq = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float2 a = lst[(v * NB + blk / NB) * 64 + r], b = lst[(v * NB + blk / NB) * 64 + r + 32];
+            sx += a.x + b.x;
+            sq += a.y + b.y;
+        }
+        const float mean = sx / (float) p.K;
+        const float var = fmaxf(sq / (float) p.K - mean * mean, 0.0f);
+        const float inv = 1.0f / sqrtf(var + p.lnf_eps);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[g * 4 + e] = inv * (sum[g * 4 + e] - mean * lc1[g * 4 + e]);
+    }
     if constexpr (ROPE) {   // the rope entry point's guarantees: N % 4, rope_d % 4, ldc == N, no residual
         store_block_rope(p, m, n0 + (blk % NB) * 32, lane, sum, rblk);
         return;
@@ -2577,6 +2656,43 @@ extern "C" void matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *a, const hexlib
     p.rope_cols = (int) rope_cols;
     p.rope_d = rope_dim;
     launch<B_NK>(p, 1, true, true);
+}
+
+// A LayerNorm folded into the W^T linear that consumes it (one launch, no
+// normalised activation stored): x is the LayerNorm's input, wt the
+// weight-scaled W'^T and bias2 = [c2 | c1] (2N floats), see gemm_nk_kw's LNF.
+// Preconditions of the K-across-waves form: K % 256 == 0, 16-byte aligned x
+// and wt; the rope form adds the rope entry point's.
+static bool lnf_ok(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2, const hexlib_hf *out, int M, int K,
+            int N, int act) {
+    return x && wt && bias2 && out && dims_ok(M, K, N, 1) && act >= 0 && act <= 2 && K % KW_BK == 0 &&
+           hx::aligned(x, 16) && hx::aligned(wt, 16);
+}
+
+extern "C" void lnfold_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2,
+                                                  hexlib_hf *out, int M, int K, int N, int act, float eps) {
+    if (!lnf_ok(x, wt, bias2, out, M, K, N, act)) return;
+    GemmArgs p = args(x, K, 0, wt, K, 0, bias2, out, N, 0, M, N, K, act);
+    p.lnf_eps = eps;
+    const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
+    HX_LAUNCH((gemm_nk_kw<64, false, false, 0, true>), grid, dim3(TPB), 0, p);
+}
+
+extern "C" void lnfold_matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2,
+                                                       const float *costab, const float *sintab, hexlib_hf *out,
+                                                       int M, int K, int N, int act, int rope_heads, int rope_dim,
+                                                       float eps) {
+    if (!lnf_ok(x, wt, bias2, out, M, K, N, act) || !costab || !sintab) return;
+    const long long rope_cols = 2LL * rope_heads * rope_dim;
+    if (rope_heads <= 0 || rope_dim <= 0 || rope_dim % 4 || rope_cols > N || N % 4 || !hx::aligned(out, 8)) return;
+    GemmArgs p = args(x, K, 0, wt, K, 0, bias2, out, N, 0, M, N, K, act);
+    p.rcos = costab;
+    p.rsin = sintab;
+    p.rope_cols = (int) rope_cols;
+    p.rope_d = rope_dim;
+    p.lnf_eps = eps;
+    const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
+    HX_LAUNCH((gemm_nk_kw<64, true, false, 0, true>), grid, dim3(TPB), 0, p);
 }
 
 // LayerNorm over K then the W^T linear, in one launch. Preconditions of the

@@ -54,6 +54,8 @@ KIND_ID: dict[str, int] = {
     "attention_qkv": 23,
     "layernorm_matmul_epilogue_f16wt": 24,
     "matmul_epilogue_q8k": 25,
+    "lnfold_matmul_epilogue_f16wt": 26,
+    "lnfold_matmul_epilogue_f16wt_rope": 27,
 }
 
 
@@ -322,6 +324,31 @@ SPECS: dict[str, RunnerSpec] = {
         weight=(3, "fp16"), rank=2,
         notes="extension: layernorm over K then the W^T linear, one launch "
               "(fused by hexlib_amd.graph.fuse.fuse_layernorm)"),
+    "lnfold_matmul_epilogue_f16wt": RunnerSpec(
+        "lnfold_matmul_epilogue", "lnfold_matmul_epilogue_f16wt_fp16", ("fp16", "fp16", "fp32"), "fp16",
+        _MM_SCALARS + (_S("attr:eps", "eps", "float"),),
+        layouts=("row_major", "col_major", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "2*(uint64_t)N", "(uint64_t)M*N"),
+        checks=("K % 256 == 0",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0"),
+        weight=(1, "fp16"), primary=False, rank=2,
+        notes="extension: a layernorm folded into the W^T linear that consumes it "
+              "(hexlib_amd.graph.fuse.fold_layernorm): weight-scaled W', bias2 = [c2 | c1]"),
+    "lnfold_matmul_epilogue_f16wt_rope": RunnerSpec(
+        "lnfold_matmul_epilogue", "lnfold_matmul_epilogue_f16wt_rope_fp16",
+        ("fp16", "fp16", "fp32", "fp32", "fp32"), "fp16",
+        _MM_SCALARS + (_S("attr:rope_heads", "rope_heads"), _S("attr:rope_dim", "rope_dim"),
+                       _S("attr:eps", "eps", "float")),
+        layouts=("row_major", "col_major_rope", "row_major", "col_major", "col_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "2*(uint64_t)N", "(uint64_t)M*rope_dim",
+                 "(uint64_t)M*rope_dim", "(uint64_t)M*N"),
+        checks=("K % 256 == 0", "N % 4 == 0", "rope_dim % 4 == 0",
+                "2LL * rope_heads * rope_dim <= N",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 15) == 0",
+                "((uintptr_t)a->buf[5] & 7) == 0"),
+        weight=(1, "fp16"), primary=False, rank=2,
+        notes="extension: the folded layernorm with the q/k rope of the fused q/k/v linear in the "
+              "epilogue (fold_layernorm after fuse_rope)"),
     "attention_qkv": RunnerSpec(
         "attention", "attention_qkv_fp16", ("fp16",), "fp16",
         (_S("dim:0:0", "rows"), _S("dim:0:2", "H"), _S("dim:0:3", "D"),

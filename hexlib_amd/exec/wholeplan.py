@@ -32,7 +32,7 @@ import numpy as np
 
 from hexlib_amd.exec import wire
 from hexlib_amd.exec.runner import KIND_ID, WIRE_RAW, RunnerSpec, select
-from hexlib_amd.graph.fuse import fuse, fuse_layernorm, fuse_residual, fuse_rope
+from hexlib_amd.graph.fuse import LNFOLD_RECIPES, fold_layernorm, fuse, fuse_layernorm, fuse_residual, fuse_rope
 from hexlib_amd.graph.ir import Graph
 from hexlib_amd.graph.ir import nbytes as ir_nbytes
 from hexlib_amd.quant import pack_q4_0_kgrouped, pack_q4_0_nblocked, pack_q8_0_kgrouped
@@ -147,19 +147,34 @@ def _reuse_offsets(g: Graph, acts, reshape_src, owner, wbytes) -> tuple[dict[str
 def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                            weight_layout: str | None = "auto", fuse_first: bool = True,
                            fd: int = 0, reuse: bool = True, residual: bool = False,
-                           rope: bool = False, layernorm: bool = False) -> WholePlanBatch:
+                           rope: bool = False, layernorm: bool = False,
+                           fold_ln_rows: int = 0) -> WholePlanBatch:
     """`residual=True` also folds each residual add into the fp16 linear that
     feeds it (`fuse_residual`), `rope=True` the q/k rope of a fused q/k/v
     projection into that linear (`fuse_rope`) and `layernorm=True` each
-    LayerNorm into the linear it feeds (`fuse_layernorm`), when fp16 weights
-    are staged transposed (the only layout with those kernels)."""
+    LayerNorm into the linear it feeds (`fuse_layernorm`, the normalised rows
+    recomputed in the linear's prologue), when fp16 weights are staged
+    transposed (the only layout with those kernels). `fold_ln_rows > 0` folds
+    each LayerNorm of at most that many rows into the linear it feeds
+    algebraically instead (`fold_layernorm`: weight-scaled W' and bias
+    vectors derived here from the feeds, row statistics in the GEMM)."""
     g = fuse(graph) if fuse_first else graph
     if rope and weight_layout in ("auto", "col_major"):
         g = fuse_rope(g)
     if residual and weight_layout in ("auto", "col_major"):
         g = fuse_residual(g)
+    derived: dict = {}
+    if fold_ln_rows > 0 and weight_layout in ("auto", "col_major"):
+        g, derived = fold_layernorm(g, max_rows=fold_ln_rows)
     if layernorm and weight_layout in ("auto", "col_major"):
         g = fuse_layernorm(g)
+    if derived:
+        feeds = dict(feeds)
+        for n, (recipe, srcs) in derived.items():
+            missing = [s for s in srcs if s not in feeds]
+            if missing:
+                raise WholePlanError(f"no feed for {missing[0]!r} (needed by derived {n!r})")
+            feeds[n] = LNFOLD_RECIPES[recipe](*(feeds[s] for s in srcs))
     tensors = g.tensors
     io = set(g.inputs) | set(g.outputs)
     consts = {n for n, t in tensors.items() if t.const}

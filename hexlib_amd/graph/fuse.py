@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import math
 
-from hexlib_amd.graph.ir import Graph, Op
+from hexlib_amd.graph.ir import Graph, Op, Tensor
 
 FUSABLE_ACTS = ("gelu_tanh", "gelu_erf")
 
@@ -212,3 +212,104 @@ def fuse_layernorm(graph: Graph, max_rows: int = 2048) -> Graph:
     ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
     tensors = {n: t for n, t in graph.tensors.items() if n not in dropped}
     return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)
+
+
+# ---- LayerNorm folded into the linear it feeds -----------------------------------
+#
+# LN(x) = (x - mean) rstd * w + b over the last axis, then y = LN(x) W + bias:
+#   y = rstd (x W' - mean c1) + c2,  W'[k][n] = fp16(w[k] W[k][n]),
+#   c1[n] = sum_k W'[k][n],  c2[n] = bias[n] + sum_k b[k] W[k][n].
+# The kernel (lnfold_matmul_epilogue) multiplies the raw x by W' and takes each
+# row's mean and rstd from the x tiles it reads, so the LayerNorm needs no
+# launch of its own and its fp16 output is never stored. W' and bias2 = [c2|c1]
+# are new consts derived from the plan's weights when the plan is staged.
+
+LNFOLD_WEIGHT = "lnfold_weight"   # W' from (W, ln_w)
+LNFOLD_BIAS2 = "lnfold_bias2"     # [c2 | c1] from (W, ln_w, ln_b, bias)
+
+
+def lnfold_weight(w, ln_w):
+    """W' = fp16(ln_w[k] * W[k][n]): the exact product rounded once to fp16."""
+    import numpy as np
+    return (np.asarray(w, dtype=np.float64) * np.asarray(ln_w, dtype=np.float64)[:, None]).astype(np.float16)
+
+
+def lnfold_bias2(w, ln_w, ln_b, bias):
+    """[c2 | c1] as 2N fp32: c2 = bias + ln_b W (float64, rounded once), c1 the
+    column sums of the rounded W' (float64, rounded once)."""
+    import numpy as np
+    w64 = np.asarray(w, dtype=np.float64)
+    c1 = lnfold_weight(w, ln_w).astype(np.float64).sum(axis=0)
+    c2 = np.asarray(bias, dtype=np.float64) + np.asarray(ln_b, dtype=np.float64) @ w64
+    return np.concatenate([c2, c1]).astype(np.float32)
+
+
+LNFOLD_RECIPES = {LNFOLD_WEIGHT: lnfold_weight, LNFOLD_BIAS2: lnfold_bias2}
+
+
+def fold_layernorm(graph: Graph, max_rows: int = 256) -> tuple[Graph, dict[str, tuple[str, tuple[str, ...]]]]:
+    """Fold each LayerNorm whose only reader is an fp16 linear (plain, or with
+    the q/k rope in its epilogue) into that linear: the pair becomes one
+    `lnfold_matmul_epilogue` op reading the LayerNorm's input. Applies where
+    the kernel's form does -- K % 256 == 0 -- and up to `max_rows` rows, the
+    sizes its 64x64 K-across-waves tiles fill the GPU at; elsewhere the
+    LayerNorm stays a launch of its own.
+
+    Returns the new graph and the derived consts it reads, `{name: (recipe,
+    source names)}` with the recipe a key of `LNFOLD_RECIPES`; the plan
+    builder computes their values from the feeds."""
+    readers: dict[str, list[Op]] = {}
+    for op in graph.ops:
+        for name in op.inputs:
+            readers.setdefault(name, []).append(op)
+    outputs = set(graph.outputs)
+    tensors = dict(graph.tensors)
+    replaced: dict[int, Op] = {}
+    absorbed: set[int] = set()
+    dropped: set[str] = set()
+    derived: dict[str, tuple[str, tuple[str, ...]]] = {}
+    for ln in graph.ops:
+        if ln.kind != "layernorm" or len(ln.inputs) != 3:
+            continue
+        x_name, lw, lb = ln.inputs
+        y = ln.outputs[0]
+        users = readers.get(y, [])
+        if y in outputs or len(users) != 1:
+            continue
+        mm = users[0]
+        if mm.kind != "matmul_epilogue" or mm.inputs[0] != y or len(mm.inputs) not in (3, 5):
+            continue
+        rope = len(mm.inputs) == 5
+        if rope and "rope_heads" not in mm.attrs:
+            continue
+        w_name, b_name = mm.inputs[1], mm.inputs[2]
+        w, b = graph.tensor(w_name), graph.tensor(b_name)
+        x = graph.tensor(x_name)
+        if not (w.const and b.const and graph.tensor(lw).const and graph.tensor(lb).const):
+            continue
+        if w.dtype != "fp16" or len(w.shape) != 2 or len(b.shape) != 1 or len(x.shape) != 2:
+            continue
+        rows, feats = x.shape
+        if feats % 256 or rows > max_rows or w.shape[0] != feats or y in mm.inputs[1:]:
+            continue
+        n = w.shape[1]
+        wf, b2 = f"lnfold{mm.id}.w", f"lnfold{mm.id}.bias2"
+        if wf in tensors or b2 in tensors:
+            raise FuseError(f"fold_layernorm: names {wf!r} / {b2!r} are taken")
+        tensors[wf] = Tensor(wf, "fp16", (feats, n), const=True)
+        tensors[b2] = Tensor(b2, "fp32", (2 * n,), const=True)
+        derived[wf] = (LNFOLD_WEIGHT, (w_name, lw))
+        derived[b2] = (LNFOLD_BIAS2, (w_name, lw, lb, b_name))
+        attrs = {k: v for k, v in dict(mm.attrs).items() if k != "round"}
+        attrs["eps"] = ln.attrs["eps"]
+        replaced[mm.id] = Op(id=mm.id, kind="lnfold_matmul_epilogue",
+                             inputs=(x_name, wf, b2) + tuple(mm.inputs[3:]), outputs=mm.outputs,
+                             attrs=attrs)
+        absorbed.add(ln.id)
+        dropped.add(y)
+    if not replaced:
+        return graph, {}
+    ops = tuple(replaced.get(op.id, op) for op in graph.ops if op.id not in absorbed)
+    used = {n for op in ops for n in op.inputs + op.outputs} | set(graph.inputs) | set(graph.outputs)
+    tensors = {n: t for n, t in tensors.items() if n not in dropped and n in used}
+    return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs), derived

@@ -43,6 +43,8 @@ SIGNATURES = {
     "matmul_epilogue_f16wt_rope_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "attention_qkv_fp16": (None, [_P, _P, _I, _I, _I, _I, _F]),
     "layernorm_matmul_epilogue_f16wt_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F]),
+    "lnfold_matmul_epilogue_f16wt_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F]),
+    "lnfold_matmul_epilogue_f16wt_rope_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F]),
     "attention_fp16": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F]),
     "attention_qk_v_fp16": (None, [_P, _P, _P, _I, _I, _I, _I, _F]),
     "rope_2d_qk_fp16": (None, [_P, _P, _P, _P, _I, _I, _I]),

@@ -283,6 +283,27 @@ void attention_qkv_fp16(const hexlib_hf *qkv, hexlib_hf *out, int rows, int H, i
 void layernorm_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const float *ln_w, const float *ln_b,
                                           const hexlib_hf *wt, const float *bias, hexlib_hf *out,
                                           int M, int K, int N, int act, float eps);
+/* A LayerNorm (eps) folded into the W^T linear that consumes it, one launch
+ * and no normalised activation in memory (KIND 26). x [M, K] is the
+ * LayerNorm's raw input; wt [N, K] holds W' = fp16(ln_w[k] * W[k][n])
+ * transposed; bias2 holds 2N floats: c2[n] = bias[n] + sum_k ln_b[k] W[k][n],
+ * then c1[n] = sum_k W'[k][n]. out = act(rstd (x W' - mean c1) + c2), with
+ * each row's mean and one-pass variance taken in fp32 from the x tiles the
+ * product reads. Within the GEMM tolerance of layernorm_fp16 followed by
+ * matmul_epilogue_f16wt_fp16, not bit-identical to them. No reference
+ * counterpart: the fusion of kernels/layernorm_fp16/kernel_api.h:38-39 into
+ * the linear that consumes it. Requires K % 256 == 0 and 16-byte aligned x
+ * and wt; else a no-op. */
+void lnfold_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2,
+                                       hexlib_hf *out, int M, int K, int N, int act, float eps);
+/* The same with the q/k rope of matmul_epilogue_f16wt_rope_fp16 in the
+ * epilogue (KIND 27): wt in that entry's pair-interleaved col_major_rope
+ * layout, c1 and c2 indexed by output feature as its bias is. Adds that
+ * entry's requirements. */
+void lnfold_matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2,
+                                            const float *costab, const float *sintab, hexlib_hf *out,
+                                            int M, int K, int N, int act, int rope_heads, int rope_dim,
+                                            float eps);
 
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
@@ -309,6 +330,8 @@ int attention_qk_v_fp16_entry(const hexlib_args *a);
 int rope_2d_qk_fp16_entry(const hexlib_args *a);
 int layernorm_matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q8k_fp16_entry(const hexlib_args *a);
+int lnfold_matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
+int lnfold_matmul_epilogue_f16wt_rope_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

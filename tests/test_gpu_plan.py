@@ -30,10 +30,10 @@ def session(torch_gpu):
 
 
 def _run_plan(session, cfg, feeds, graph_mode, weight_layout=None, repeats=1, residual=False, rope=False,
-              layernorm=False):
+              layernorm=False, fold_ln_rows=0):
     g = E.build_vision_encoder(cfg)
     wb = build_whole_plan_batch(g, feeds, weight_layout=weight_layout, residual=residual, rope=rope,
-                                layernorm=layernorm)
+                                layernorm=layernorm, fold_ln_rows=fold_ln_rows)
     plan = GpuPlan(wb, session)
     try:
         outs = []
@@ -273,6 +273,31 @@ def test_fused_attention_encoder_matches_the_reference_graph(session, image, bat
     err = np.abs(out - want).max()
     print(f"[{mode} residual={residual} rope={rope} ln={ln} {image} b{batch}] max abs vs reference graph "
           f"{err:.3e}", flush=True)
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize("image,batch", [(256, 1), (256, 4), (448, 1)])
+def test_folded_layernorm_plan_matches_the_reference_graph(session, image, batch):
+    """The bench's batch-1 product plan -- fused q/k/v + rope, fused
+    attention, residual epilogues, and every block LayerNorm folded into the
+    linear it feeds (66 launches at batch 1) -- here also at batch 4 and at
+    448x448 with the fold allowed at those row counts: against the storage-
+    rounding oracle of the REFERENCE graph, <= 2e-2 max abs; graph replays
+    equal to each other bit for bit."""
+    base = E.QWEN35_VISION_FP16 if image == 256 else E.encoder_at(image)
+    cfg_ref = replace(base, batch=batch)
+    g_ref = E.build_vision_encoder(cfg_ref)
+    feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=5)
+    cfg = replace(cfg_ref, attention="fused_qkv_rope")
+    outs, wb = _run_plan(session, cfg, E.fuse_qkv_feeds(feeds, cfg), graph_mode=True, repeats=3, residual=True,
+                         rope=True, weight_layout="auto", fold_ln_rows=cfg.num_tokens * batch)
+    assert wb.n_ops == 259 - 12 * 11 - 25 - 12 - 24
+    assert sum(s.startswith("lnfold_matmul_epilogue") for s in wb.op_specs) == 24
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    want = _oracle(cfg_ref, feeds)
+    err = np.abs(outs[0] - want).max()
+    print(f"[folded layernorm {image} b{batch}] max abs vs reference graph {err:.3e}", flush=True)
     assert err <= 2e-2
 
 
