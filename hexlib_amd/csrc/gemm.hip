@@ -1074,6 +1074,47 @@ struct RopeBlock {
     float2 c0[4], c1[4], s0[4], s1[4];
 };
 
+// The 16 per-column values a lane needs for its 4 groups of 4 accumulator
+// columns of the 32-column block at nb (column nb + 8 g + 4 (lane / 32) + e),
+// from `src` indexed by output feature: a rope head's pair-interleaved columns
+// hold features lo, hi, lo + 1, hi + 1 (rope_quad). A plain block (32
+// consecutive features) is read with wave-uniform scalar loads, tracked apart
+// from the vector loads of the ring (the folded fc1 at batch 1: 6.97 -> 6.67
+// us against per-lane loads); a rope block keeps per-lane loads (scalar
+// windows measured slower there).
+__device__ __forceinline__ void load_block_cols(const GemmArgs &p, const float *src, int nb, int lane,
+                                                float (&out)[16]) {
+    typedef const __attribute__((address_space(4))) float cfloat;
+    const int nbu = __builtin_amdgcn_readfirstlane(nb);
+    const int hi = lane >> 5;
+    const bool rope_blk = p.rcos && nbu < p.rope_cols;
+    if (!rope_blk && nbu + 32 <= p.N) {
+        const cfloat *c = reinterpret_cast<const cfloat *>(reinterpret_cast<uintptr_t>(src + nbu));
+        float w[32];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) w[k] = c[k];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[g * 4 + e] = hi ? w[g * 8 + 4 + e] : w[g * 8 + e];
+        return;
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + hi * 4;
+        int f[4] = {n, n + 1, n + 2, n + 3};
+        if (p.rcos && n < p.rope_cols) {
+            const RopeQuad q = rope_quad(n, p.rope_d);
+            f[0] = q.lo;
+            f[1] = q.hi;
+            f[2] = q.lo + 1;
+            f[3] = q.hi + 1;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[g * 4 + e] = n + e < p.N ? src[f[e]] : 0.0f;
+    }
+}
+
 template <int RD>
 __device__ __forceinline__ RopeBlock rope_block_load(const GemmArgs &p, int m, int nb, int lane) {
     const int rope_d = RD ? RD : p.rope_d;   // RD: the head width fixed at compile time (0: runtime)
@@ -1145,21 +1186,7 @@ __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int n
 // or, for a rope head's pair-interleaved columns, the output feature that
 // column holds (the bias's own index, as rope_block_load takes it).
 __device__ __forceinline__ void load_block_c1(const GemmArgs &p, int nb, int lane, float (&c1)[16]) {
-    const float *src = p.bias + p.N;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int n = nb + g * 8 + (lane >> 5) * 4;
-        int f[4] = {n, n + 1, n + 2, n + 3};
-        if (p.rcos && n < p.rope_cols) {
-            const RopeQuad q = rope_quad(n, p.rope_d);
-            f[0] = q.lo;
-            f[1] = q.hi;
-            f[2] = q.lo + 1;
-            f[3] = q.hi + 1;
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) c1[g * 4 + e] = n + e < p.N ? src[f[e]] : 0.0f;
-    }
+    load_block_cols(p, p.bias + p.N, nb, lane, c1);
 }
 
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
