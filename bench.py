@@ -87,17 +87,26 @@ def gemm_bytes(in_shapes, in_dtypes, out_shape) -> float:
 
 # ---- plan helpers -------------------------------------------------------------------------
 
-FOLD_LN_ROWS = 256
+def fold_rule(rows: int) -> bool:
+    """Where folding a LayerNorm into its linear pays on MI355X: up to 256 rows
+    (the 64x64 K-across-waves form fills the chip: batch 1 at 256x256) and from
+    2048 rows (the large-tile form's tiles fill a round of CUs: batch 32). In
+    between (448x448, 784 rows) the tiled kernel the unfused linear takes is
+    faster than either folded form."""
+    return rows <= 256 or rows >= 2048
+
+
+FOLD_LN_ROWS = fold_rule
 
 
 def build_plan(cfg, seed=0, weight_layout="auto", residual=True, rope=True, layernorm=False,
                fold_ln_rows=None):
     """The product plan: fusions on (`residual` folds residual adds into the
     fp16 linears, `rope` the q/k rope into the fused q/k/v linear; the
-    config's `attention` picks the attention form). Each LayerNorm of at most
-    `fold_ln_rows` rows (default FOLD_LN_ROWS: the batch-1 256x256 plan) is
-    folded algebraically into the linear it feeds (`fold_layernorm`: no
-    launch of its own). `layernorm` (the normalised rows recomputed in the
+    config's `attention` picks the attention form). Each LayerNorm whose row
+    count `fold_ln_rows` admits (default FOLD_LN_ROWS: `fold_rule`) is folded
+    algebraically into the linear it feeds (`fold_layernorm`: no launch of its
+    own). `layernorm` (the normalised rows recomputed in the
     linear's prologue) is off: every workgroup of that
     kernel normalises its whole row block again, 48 times per row at fc1,
     which costs more than the separate launch it saves (18.6 us against
@@ -838,8 +847,8 @@ def main() -> int:
                          "same shapes, print them and exit (the rocprofv3 --pmc target for those GEMMs)")
     ap.add_argument("--no-library", action="store_true", help="with --gemm-b32: skip torch.matmul")
     ap.add_argument("--fold-ln-rows", type=int, default=None,
-                    help="fold LayerNorms of at most this many rows into their linear (default "
-                         f"{FOLD_LN_ROWS}; 0: every LayerNorm its own launch)")
+                    help="fold LayerNorms of at most this many rows into their linear (default: "
+                         "fold_rule; 0: every LayerNorm its own launch)")
     ap.add_argument("--plan-only", metavar="VARIANT",
                     choices=("256_b1", "256_b32", "448_b1", "256_b1_q8_0", "256_b1_q4_0"),
                     help="build that plan, time --steps graph replays of it and exit (a rocprofv3 "

@@ -1571,22 +1571,54 @@ __device__ __forceinline__ void big_rope_tables(const GemmArgs &p, int m0, int w
     }
 }
 
-template <int ACT, int BM, int BN, int TM, int TN, int EROW>
+// The folded LayerNorm's statistics of the large-tile kernel, after the K
+// loop: sum x (from wave column 0) and sum x^2 (wave column 1) of each lane's
+// rows, as float2 [tile row][lane / 32], written in the first epilogue pass
+// after its first barrier (the ring is free then) and read after its second.
+template <int BM, int TM>
+__device__ __forceinline__ void big_lnf_put(float2 *lst, int wave, int lane, const float (&xs)[TM],
+                                            const float (&xq)[TM]) {
+    constexpr int WN = 2;
+    const int wm = (wave / WN) * (BM / 2), r = lane & 31;
+    float *dst = reinterpret_cast<float *>(lst);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) dst[((wm + i * 32 + r) * 2 + (lane >> 5)) * 2 + wave % WN] = wave % WN ? xq[i] : xs[i];
+}
+
+// mean and rstd of tile row tr from those pairs: fp32, one-pass variance
+// clamped at 0, as the K-across-waves form takes them
+__device__ __forceinline__ void big_lnf_row(const GemmArgs &p, const float2 *lst, int tr, float &mean, float &inv) {
+    const float2 a = lst[tr * 2], b = lst[tr * 2 + 1];
+    mean = (a.x + b.x) / (float) p.K;
+    const float var = fmaxf((a.y + b.y) / (float) p.K - mean * mean, 0.0f);
+    inv = 1.0f / sqrtf(var + p.lnf_eps);
+}
+
+template <int ACT, int BM, int BN, int TM, int TN, int EROW, bool LNF>
 __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x16 (&acc)[TN][TM], float *stage,
                                                   int m0, int n0, int wave, int lane, const float (&tt)[TM][2][2][8],
-                                                  float bias_own) {
+                                                  float bias_own, float c1_own, const float (&xs)[TM],
+                                                  const float (&xq)[TM]) {
 #pragma clang fp contract(off)
     constexpr int WN = 2, HALF = BIG_RD / 2;
     float *bias_s = stage + 64 * EROW;                     // [BN], by output feature
+    float *c1_s = bias_s + BN;                             // LNF: [BN] c1, by output feature
+    float2 *lst = reinterpret_cast<float2 *>(c1_s + BN);   // LNF: [BM][2] row sums
     const int tid = threadIdx.x, r = lane & 31;
     // bias by output feature, staged once (visible after the first pass's barrier)
     if (tid < BN) bias_s[tid] = bias_own;
+    if constexpr (LNF) {
+        if (tid < BN) c1_s[tid] = c1_own;
+    }
     const int row = wave * 16 + (lane & 15);               // this thread's staged row
     const int cq = lane >> 4;                              // its chunks: cq, cq + 4, cq + 8, ...
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         // 1. staging writes
         __builtin_amdgcn_s_barrier();              // the ring's (or the last pass's) reads are done
+        if constexpr (LNF) {
+            if (i == 0) big_lnf_put<BM, TM>(lst, wave, lane, xs, xq);
+        }
         const int srow = (wave / WN) * 32 + r;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -1600,6 +1632,13 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
         // 2. one row, four chunks
         const int m = m0 + (row >> 5) * (BM / 2) + i * 32 + (row & 31);
         if (m >= p.M) continue;
+        // LNF: the row's mean and rstd; column c's value becomes rstd (v - mean c1[c])
+        float lmean = 0.0f, linv = 1.0f;
+        if constexpr (LNF) big_lnf_row(p, lst, (row >> 5) * (BM / 2) + i * 32 + (row & 31), lmean, linv);
+        auto lnf = [&](float v, int f) {
+            if constexpr (LNF) return linv * (v - lmean * c1_s[f]);
+            else return v;
+        };
         f16 *crow = p.C + (long long) m * p.ldc;
         const float *srow_p = stage + row * EROW;
 #pragma unroll
@@ -1624,8 +1663,10 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     // computed column 2 (i0 + u) is feature i0 + u, 2 (i0 + u) + 1 is feature i0 + u + D/2
-                    const float x0 = (float) (f16) f32_rounded(act_t<ACT>(v[2 * u] + bias_s[hb + i0 + u]));
-                    const float x1 = (float) (f16) f32_rounded(act_t<ACT>(v[2 * u + 1] + bias_s[hb + i0 + u + HALF]));
+                    const float x0 =
+                        (float) (f16) f32_rounded(act_t<ACT>(lnf(v[2 * u], hb + i0 + u) + bias_s[hb + i0 + u]));
+                    const float x1 = (float) (f16) f32_rounded(
+                        act_t<ACT>(lnf(v[2 * u + 1], hb + i0 + u + HALF) + bias_s[hb + i0 + u + HALF]));
                     const float cv = ct[u], sv = st[u];
                     if (hi) {
                         const float p1 = x1 * cv, q1 = x0 * sv;
@@ -1640,8 +1681,8 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
                 const f32x4 a1 = *reinterpret_cast<const f32x4 *>(srow_p + f0 + 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    o[e] = epi_t<ACT, false>(a0[e] + bias_s[f0 + e], (f16) 0);
-                    o[e + 4] = epi_t<ACT, false>(a1[e] + bias_s[f0 + 4 + e], (f16) 0);
+                    o[e] = epi_t<ACT, false>(lnf(a0[e], f0 + e) + bias_s[f0 + e], (f16) 0);
+                    o[e + 4] = epi_t<ACT, false>(lnf(a1[e], f0 + 4 + e) + bias_s[f0 + 4 + e], (f16) 0);
                 }
             }
             *reinterpret_cast<f16x8 *>(crow + n) = o;
@@ -1649,7 +1690,12 @@ __device__ __forceinline__ void big_rope_epilogue(const GemmArgs &p, const f32x1
     }
 }
 
-template <int BM, int BN, int STAGES, bool ROPE = false>
+// LNF: a LayerNorm over A's rows folded into the product, as gemm_nk_kw's
+// LNF form: bias holds [c2 | c1], every wave sums x and x^2 over the A
+// fragments its MFMAs use (two halves per v_dot2_f32_f16; the waves of wave
+// columns 0 and 1 read the same rows, so column 0 sums x and column 1 x^2),
+// and the epilogue applies rstd (acc - mean c1) before the bias.
+template <int BM, int BN, int STAGES, bool ROPE = false, bool LNF = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntiles) {
     constexpr int NW = 4, WN = 2;
     constexpr int TM = BM / 64, TN = BN / 64;     // 32x32 blocks per wave
@@ -1660,8 +1706,12 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
     constexpr int EROW = BN + 4;                   // floats per staged row
     constexpr int RING_BYTES = STAGES * (BM + BN) * DS_ROW * 2;
     constexpr int STAGE_BYTES = 64 * EROW * 4;
-    constexpr int BIAS_BYTES = ROPE ? BN * 4 : 0;
-    constexpr int EPI_BYTES = STAGE_BYTES + BIAS_BYTES;
+    // bias (and c1) staged by output feature: the rope form's bias and LNF c1,
+    // the plain form's LNF c1 (one value per thread held through the loop, not
+    // eight: the 128 x 192 form's registers stay within two waves per SIMD)
+    constexpr int BIAS_BYTES = ROPE ? (LNF ? 2 : 1) * BN * 4 : (LNF ? BN * 4 : 0);
+    constexpr int LNF_BYTES = LNF ? BM * 2 * 8 : 0;                  // row sums [BM][2] float2
+    constexpr int EPI_BYTES = STAGE_BYTES + BIAS_BYTES + LNF_BYTES;
     constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
     // one buffer: the A ring, then the B ring; the epilogue reuses all of it
     __shared__ __attribute__((aligned(16))) f16 lds[LDS_BYTES / 2];
@@ -1688,9 +1738,11 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         b0 = *reinterpret_cast<const f32x4 *>(p.bias + n);
         b1 = *reinterpret_cast<const f32x4 *>(p.bias + n + 4);
     }
-    // the rope form's bias, loaded now
-    float bias_own = 0.0f;
+    // the rope form's bias and the LNF c1 (thread t: column n0 + t), loaded now
+    float bias_own = 0.0f, c1_own = 0.0f;
     if constexpr (ROPE) bias_own = (tid < BN && p.bias && n0 + tid < p.N) ? p.bias[n0 + tid] : 0.0f;
+    if constexpr (LNF) c1_own = (tid < BN && n0 + tid < p.N) ? p.bias[p.N + n0 + tid] : 0.0f;
+    float xs[TM] = {}, xq[TM] = {};   // LNF: this lane's row sums (rows wm + 32 i + lane % 32)
     f32x16 acc[TN][TM];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -1724,6 +1776,28 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
             for (int i = 0; i < TM; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.w[j], cur.x[i], acc[j][i], 0, 0, 0);
         interleave_reads<0, NR, NM>();
+        if constexpr (LNF) {
+            // the two waves of a wave row read the same A rows: column 0 sums x,
+            // column 1 sums x^2 (a wave-uniform branch), half the VALU each
+            const f16x2 one2 = {(f16) 1.0f, (f16) 1.0f};
+            if (__builtin_amdgcn_readfirstlane(wave % WN) == 0) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f16x2 pr = {cur.x[i][2 * u], cur.x[i][2 * u + 1]};
+                        xs[i] = __builtin_amdgcn_fdot2(pr, one2, xs[i], false);
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f16x2 pr = {cur.x[i][2 * u], cur.x[i][2 * u + 1]};
+                        xq[i] = __builtin_amdgcn_fdot2(pr, pr, xq[i], false);
+                    }
+            }
+        }
     };
 
 #pragma unroll
@@ -1778,14 +1852,22 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
         // the activation fixed at compile time: a runtime switch per output
         // would split the unrolled epilogue into a branch per element
         dispatch_epi(p.act, false, [&](auto act_c, auto) {
-            big_rope_epilogue<decltype(act_c)::value, BM, BN, TM, TN, EROW>(p, acc, stage, m0, n0, wave, lane, tt,
-                                                                            bias_own);
+            big_rope_epilogue<decltype(act_c)::value, BM, BN, TM, TN, EROW, LNF>(p, acc, stage, m0, n0, wave, lane,
+                                                                                 tt, bias_own, c1_own, xs, xq);
         });
         return;
     }
+    float *c1_s = stage + 64 * EROW;                                  // LNF: [BN] c1
+    float2 *lst = reinterpret_cast<float2 *>(c1_s + BN);              // LNF: [BM][2] row sums
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         __builtin_amdgcn_s_barrier();              // the ring's (or the last pass's) reads are done
+        if constexpr (LNF) {
+            if (i == 0) {
+                big_lnf_put<BM, TM>(lst, wave, lane, xs, xq);
+                if (tid < BN) c1_s[tid] = c1_own;
+            }
+        }
         const int srow = (wave / WN) * 32 + r;     // staged row: 32 rows per wave row
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -1812,8 +1894,17 @@ __global__ __launch_bounds__(TPB) void gemm_nk_big(GemmArgs p, int gx, int ntile
                 if constexpr (RES) rn = resid(sr + RPI);
                 const int m = row_of(sr);
                 if (m >= p.M) continue;
-                const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
-                const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
+                f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8);
+                f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + sr * EROW + c8 + 4);
+                if constexpr (LNF) {
+                    float mean, inv;
+                    big_lnf_row(p, lst, (sr >> 5) * (BM / 2) + i * 32 + (sr & 31), mean, inv);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v0[e] = inv * (v0[e] - mean * c1_s[c8 + e]);
+                        v1[e] = inv * (v1[e] - mean * c1_s[c8 + 4 + e]);
+                    }
+                }
                 f16x8 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -2696,11 +2787,36 @@ static bool lnf_ok(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2, 
            hx::aligned(x, 16) && hx::aligned(wt, 16);
 }
 
+// Many rows (the large-tile kernel's tile fills a round of CUs): its LNF form,
+// on the 128 x 192 or 128 x 128 tile big_auto picks, where its epilogue's
+// preconditions hold (N % 8 == 0, 16-byte aligned output and bias2; the rope
+// form 64-wide heads). Returns false to leave the launch to the K-across-waves
+// form.
+static bool launch_big_lnf(const GemmArgs &p) {
+    const Tile t = big_auto(p.M, p.N, true);
+    if (!t.bm || p.N % 8 || p.ldc % 8 || !hx::aligned(p.C, 16) || !hx::aligned(p.bias, 16)) return false;
+    if (p.rcos && (p.rope_d != BIG_RD || p.rope_cols % 8)) return false;
+    const int gx = (p.N + t.bn - 1) / t.bn, gy = (p.M + t.bm - 1) / t.bm;
+    const long long nt = (long long) gx * gy;
+    if (nt > 0x7fffffffLL) return false;
+    const dim3 grid((unsigned) nt), block(TPB);
+    const int n = (int) nt;
+    if (t.bn == 192) {
+        if (p.rcos) HX_LAUNCH((gemm_nk_big<128, 192, 2, true, true>), grid, block, 0, p, gx, n);
+        else HX_LAUNCH((gemm_nk_big<128, 192, 2, false, true>), grid, block, 0, p, gx, n);
+    } else {
+        if (p.rcos) HX_LAUNCH((gemm_nk_big<128, 128, 2, true, true>), grid, block, 0, p, gx, n);
+        else HX_LAUNCH((gemm_nk_big<128, 128, 2, false, true>), grid, block, 0, p, gx, n);
+    }
+    return true;
+}
+
 extern "C" void lnfold_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2,
                                                   hexlib_hf *out, int M, int K, int N, int act, float eps) {
     if (!lnf_ok(x, wt, bias2, out, M, K, N, act)) return;
     GemmArgs p = args(x, K, 0, wt, K, 0, bias2, out, N, 0, M, N, K, act);
     p.lnf_eps = eps;
+    if (launch_big_lnf(p)) return;
     const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
     HX_LAUNCH((gemm_nk_kw<64, false, false, 0, true>), grid, dim3(TPB), 0, p);
 }
@@ -2718,6 +2834,7 @@ extern "C" void lnfold_matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *x, const
     p.rope_cols = (int) rope_cols;
     p.rope_d = rope_dim;
     p.lnf_eps = eps;
+    if (launch_big_lnf(p)) return;
     const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
     HX_LAUNCH((gemm_nk_kw<64, true, false, 0, true>), grid, dim3(TPB), 0, p);
 }

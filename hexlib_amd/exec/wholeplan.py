@@ -148,23 +148,24 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                            weight_layout: str | None = "auto", fuse_first: bool = True,
                            fd: int = 0, reuse: bool = True, residual: bool = False,
                            rope: bool = False, layernorm: bool = False,
-                           fold_ln_rows: int = 0) -> WholePlanBatch:
+                           fold_ln_rows=0) -> WholePlanBatch:
     """`residual=True` also folds each residual add into the fp16 linear that
     feeds it (`fuse_residual`), `rope=True` the q/k rope of a fused q/k/v
     projection into that linear (`fuse_rope`) and `layernorm=True` each
     LayerNorm into the linear it feeds (`fuse_layernorm`, the normalised rows
     recomputed in the linear's prologue), when fp16 weights are staged
-    transposed (the only layout with those kernels). `fold_ln_rows > 0` folds
-    each LayerNorm of at most that many rows into the linear it feeds
-    algebraically instead (`fold_layernorm`: weight-scaled W' and bias
-    vectors derived here from the feeds, row statistics in the GEMM)."""
+    transposed (the only layout with those kernels). `fold_ln_rows` (an int
+    > 0: at most that many rows; or a predicate on the row count) folds each
+    LayerNorm it admits into the linear it feeds algebraically instead
+    (`fold_layernorm`: weight-scaled W' and bias vectors derived here from the
+    feeds, row statistics in the GEMM)."""
     g = fuse(graph) if fuse_first else graph
     if rope and weight_layout in ("auto", "col_major"):
         g = fuse_rope(g)
     if residual and weight_layout in ("auto", "col_major"):
         g = fuse_residual(g)
     derived: dict = {}
-    if fold_ln_rows > 0 and weight_layout in ("auto", "col_major"):
+    if (callable(fold_ln_rows) or fold_ln_rows > 0) and weight_layout in ("auto", "col_major"):
         g, derived = fold_layernorm(g, max_rows=fold_ln_rows)
     if layernorm and weight_layout in ("auto", "col_major"):
         g = fuse_layernorm(g)

@@ -247,13 +247,14 @@ def lnfold_bias2(w, ln_w, ln_b, bias):
 LNFOLD_RECIPES = {LNFOLD_WEIGHT: lnfold_weight, LNFOLD_BIAS2: lnfold_bias2}
 
 
-def fold_layernorm(graph: Graph, max_rows: int = 256) -> tuple[Graph, dict[str, tuple[str, tuple[str, ...]]]]:
+def fold_layernorm(graph: Graph, max_rows=256) -> tuple[Graph, dict[str, tuple[str, tuple[str, ...]]]]:
     """Fold each LayerNorm whose only reader is an fp16 linear (plain, or with
     the q/k rope in its epilogue) into that linear: the pair becomes one
     `lnfold_matmul_epilogue` op reading the LayerNorm's input. Applies where
-    the kernel's form does -- K % 256 == 0 -- and up to `max_rows` rows, the
-    sizes its 64x64 K-across-waves tiles fill the GPU at; elsewhere the
-    LayerNorm stays a launch of its own.
+    the kernel's forms do -- K % 256 == 0 -- and at the row counts `max_rows`
+    admits: an int (at most that many rows) or a predicate on the row count
+    (the caller's choice of where the fold pays); elsewhere the LayerNorm
+    stays a launch of its own.
 
     Returns the new graph and the derived consts it reads, `{name: (recipe,
     source names)}` with the recipe a key of `LNFOLD_RECIPES`; the plan
@@ -290,7 +291,8 @@ def fold_layernorm(graph: Graph, max_rows: int = 256) -> tuple[Graph, dict[str, 
         if w.dtype != "fp16" or len(w.shape) != 2 or len(b.shape) != 1 or len(x.shape) != 2:
             continue
         rows, feats = x.shape
-        if feats % 256 or rows > max_rows or w.shape[0] != feats or y in mm.inputs[1:]:
+        rows_ok = max_rows(rows) if callable(max_rows) else rows <= max_rows
+        if feats % 256 or not rows_ok or w.shape[0] != feats or y in mm.inputs[1:]:
             continue
         n = w.shape[1]
         wf, b2 = f"lnfold{mm.id}.w", f"lnfold{mm.id}.bias2"

@@ -301,6 +301,27 @@ def test_folded_layernorm_plan_matches_the_reference_graph(session, image, batch
     assert err <= 2e-2
 
 
+def test_folded_layernorm_product_plan_at_batch_32(session):
+    """The batch-32 product plan with every block LayerNorm folded into the
+    linear it feeds (the large-tile form's KIND 26 / 27): images 0 and 31
+    against the storage-rounding oracle of the REFERENCE graph at batch 1 on
+    that image's feeds, <= 2e-2 max abs."""
+    cfg1 = E.QWEN35_VISION_FP16
+    cfg_ref = replace(cfg1, batch=32)
+    g_ref = E.build_vision_encoder(cfg_ref)
+    feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=7)
+    cfg = replace(cfg_ref, attention="fused_qkv_rope")
+    (out,), wb = _run_plan(session, cfg, E.fuse_qkv_feeds(feeds, cfg), graph_mode=True, residual=True,
+                           rope=True, weight_layout="auto", fold_ln_rows=32 * cfg1.num_tokens)
+    assert wb.n_ops == 259 - 12 * 11 - 25 - 12 - 24
+    per = out.shape[0] // 32
+    for i in (0, 31):
+        want = _oracle(cfg1, _image_feeds(cfg1, feeds, i))
+        err = np.abs(out[i * per:(i + 1) * per] - want).max()
+        print(f"[folded layernorm b32] image {i}: max abs vs reference graph {err:.3e}", flush=True)
+        assert err <= 2e-2
+
+
 def _image_feeds(cfg1, feeds_b, i):
     """Image i's feeds at batch 1, sliced from a batch's feeds: its channels of
     the stacked image, its rows of the per-token tables, every const shared."""
