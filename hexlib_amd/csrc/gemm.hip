@@ -2335,7 +2335,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_q16(GemmArgs p) {
         const int m = 4 * c + i;
         if (m >= p.M || n >= p.N) continue;
         if constexpr (SPLIT) p.ws[((long long) blockIdx.y * p.M + m) * p.N + n] = v;
-        else p.C[(long long) m * p.ldc + n] = epi(v + bias, p.act, false, (f16) 0);
+        else p.C[(long long) m * p.ldc + n] = epi(v + bias, p.act, p.R, p.R ? p.R[(long long) m * p.ldr + n] : (f16) 0);
     }
 }
 
@@ -2492,8 +2492,7 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
                 const dim3 grid((unsigned) gx, (unsigned) ks);
                 HX_LAUNCH((gemm_q16<QBM, 8, true>), grid, dim3(512), 0, p);
                 HX_LAUNCH(splitk_reduce, dim3(hx::blocks_for(((long long) p.M * p.N + 3) / 4, TPB, 4096)), dim3(TPB),
-                          0, (const float *) p.ws, p.bias, p.C, p.ldc, 0LL, p.M, p.N, ks, p.act, 1,
-                          (const f16 *) nullptr, 0LL);
+                          0, (const float *) p.ws, p.bias, p.C, p.ldc, 0LL, p.M, p.N, ks, p.act, 1, p.R, p.ldr);
                 return;
             }
             const dim3 grid((unsigned) gx);
@@ -2884,4 +2883,41 @@ extern "C" void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char
     if (!hx::aligned(wt, 2)) return;
     launch<B_Q4K>(args(a, K, 0, wt, (long long) (K / 32) * 18, 0, bias, out, N, 0, M, N, K, act), 1,
                   K % 8 == 0 && hx::aligned(a, 16), false);
+}
+
+// The quantized-weight linears with the residual add that consumes them in
+// the epilogue (act(acc + bias) rounded to fp16, then fp16(resid + that)), as
+// matmul_epilogue_f16wt_res_fp16 does for fp16 weights: every route these
+// weights take (one wave per column, the 16-row MFMA form and its split-K
+// reduce, the K-across-waves and register-staged kernels) applies it.
+extern "C" void matmul_epilogue_res_fp16(const hexlib_hf *a, const unsigned char *w, const float *bias,
+                                         const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N, int act) {
+    if (!a || !w || !resid || !out || !dims_ok(M, K, N, 1) || N % 32 || act < 0 || act > 2) return;
+    if (!hx::aligned(w, 2)) return;
+    GemmArgs p = args(a, K, 0, w, (long long) (N / 32) * 18, 0, bias, out, N, 0, M, N, K, act);
+    p.R = reinterpret_cast<const f16 *>(resid);
+    p.ldr = N;
+    launch<B_Q4N>(p, 1, K % 8 == 0 && hx::aligned(a, 16), false);
+}
+
+extern "C" void matmul_epilogue_q8k_res_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
+                                             const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N,
+                                             int act) {
+    if (!a || !wt || !resid || !out || !dims_ok(M, K, N, 1) || K % 32 || act < 0 || act > 2) return;
+    if (!hx::aligned(wt, 2)) return;
+    GemmArgs p = args(a, K, 0, wt, (long long) (K / 32) * 34, 0, bias, out, N, 0, M, N, K, act);
+    p.R = reinterpret_cast<const f16 *>(resid);
+    p.ldr = N;
+    launch<B_Q8K>(p, 1, K % 8 == 0 && hx::aligned(a, 16), false);
+}
+
+extern "C" void matmul_epilogue_q4k_res_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
+                                             const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N,
+                                             int act) {
+    if (!a || !wt || !resid || !out || !dims_ok(M, K, N, 1) || K % 32 || act < 0 || act > 2) return;
+    if (!hx::aligned(wt, 2)) return;
+    GemmArgs p = args(a, K, 0, wt, (long long) (K / 32) * 18, 0, bias, out, N, 0, M, N, K, act);
+    p.R = reinterpret_cast<const f16 *>(resid);
+    p.ldr = N;
+    launch<B_Q4K>(p, 1, K % 8 == 0 && hx::aligned(a, 16), false);
 }

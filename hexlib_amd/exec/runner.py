@@ -56,6 +56,9 @@ KIND_ID: dict[str, int] = {
     "matmul_epilogue_q8k": 25,
     "lnfold_matmul_epilogue_f16wt": 26,
     "lnfold_matmul_epilogue_f16wt_rope": 27,
+    "matmul_epilogue_res": 28,
+    "matmul_epilogue_q8k_res": 29,
+    "matmul_epilogue_q4k_res": 30,
 }
 
 
@@ -248,6 +251,30 @@ SPECS: dict[str, RunnerSpec] = {
         weight=(1, "q8_0"), primary=False,
         notes="extension: q8_0 weight, logical [K, N] on the wire, stored as W^T [N, K] blocked along K "
               "(the reference has the dtype, no kernel)"),
+    "matmul_epilogue_res": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_res_fp16", ("fp16", "q4_0", "fp32", "fp16"), "fp16",
+        _MM_SCALARS, extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N", "(uint64_t)M*N"),
+        weight=(1, "q4_0"), primary=False,
+        notes="extension: the reference-ABI q4_0 linear (blocks along N) with the residual add that "
+              "consumes it folded into the epilogue (fuse_residual)",
+        rank=2),
+    "matmul_epilogue_q8k_res": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_q8k_res_fp16", ("fp16", "q8_0", "fp32", "fp16"), "fp16",
+        _MM_SCALARS,
+        layouts=("row_major", "q8_0_kgroup", "row_major", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N", "(uint64_t)M*N"),
+        checks=("K % 32 == 0", "((uintptr_t)a->buf[1] & 1) == 0"),
+        weight=(1, "q8_0"), primary=False,
+        notes="extension: the q8_0 (K-grouped W^T) linear with the residual add in the epilogue",
+        rank=2),
+    "matmul_epilogue_q4k_res": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_q4k_res_fp16", ("fp16", "q4_0", "fp32", "fp16"), "fp16",
+        _MM_SCALARS,
+        layouts=("row_major", "q4_0_kgroup", "row_major", "row_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N", "(uint64_t)M*N"),
+        weight=(1, "q4_0"), primary=False,
+        notes="extension: the K-grouped q4_0 linear with the residual add in the epilogue",
+        rank=2),
     "matmul_epilogue_f16w": RunnerSpec(
         "matmul_epilogue", "matmul_epilogue_f16w_fp16", ("fp16", "fp16", "fp32"), "fp16",
         _MM_SCALARS, extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*N"),

@@ -149,8 +149,9 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                            fd: int = 0, reuse: bool = True, residual: bool = False,
                            rope: bool = False, layernorm: bool = False,
                            fold_ln_rows=0) -> WholePlanBatch:
-    """`residual=True` also folds each residual add into the fp16 linear that
-    feeds it (`fuse_residual`), `rope=True` the q/k rope of a fused q/k/v
+    """`residual=True` also folds each residual add into the linear that
+    feeds it (`fuse_residual`: quantized weights in any layout, fp16 weights
+    when staged transposed), `rope=True` the q/k rope of a fused q/k/v
     projection into that linear (`fuse_rope`) and `layernorm=True` each
     LayerNorm into the linear it feeds (`fuse_layernorm`, the normalised rows
     recomputed in the linear's prologue), when fp16 weights are staged
@@ -162,8 +163,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
     g = fuse(graph) if fuse_first else graph
     if rope and weight_layout in ("auto", "col_major"):
         g = fuse_rope(g)
-    if residual and weight_layout in ("auto", "col_major"):
-        g = fuse_residual(g)
+    if residual:
+        g = fuse_residual(g, fp16_weights=weight_layout in ("auto", "col_major"))
     derived: dict = {}
     if (callable(fold_ln_rows) or fold_ln_rows > 0) and weight_layout in ("auto", "col_major"):
         g, derived = fold_layernorm(g, max_rows=fold_ln_rows)

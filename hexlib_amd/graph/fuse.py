@@ -81,7 +81,11 @@ def fuse(graph: Graph) -> Graph:
     return Graph(tensors=tensors, ops=ops, inputs=graph.inputs, outputs=graph.outputs)
 
 
-def fuse_residual(graph: Graph) -> Graph:
+def fuse_residual(graph: Graph, fp16_weights: bool = True) -> Graph:
+    """Fold each residual add into the linear that feeds it (the linear's
+    output read only by the add). Quantized weights (q4_0, q8_0) take their
+    residual kernels in any layout; fp16 weights only with `fp16_weights`
+    (their residual kernel takes the weight transposed)."""
     readers: dict[str, list[Op]] = {}
     for op in graph.ops:
         for name in op.inputs:
@@ -93,7 +97,8 @@ def fuse_residual(graph: Graph) -> Graph:
     for op in graph.ops:
         if op.kind != "matmul_epilogue" or len(op.inputs) != 3 or op.id in absorbed:
             continue
-        if graph.tensor(op.inputs[1]).dtype != "fp16":
+        wdt = graph.tensor(op.inputs[1]).dtype
+        if wdt not in ("fp16", "q4_0", "q8_0") or (wdt == "fp16" and not fp16_weights):
             continue
         out = op.outputs[0]
         rd = readers.get(out, [])

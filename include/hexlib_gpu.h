@@ -306,6 +306,21 @@ void lnfold_matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *x, const hexlib_hf 
                                             int M, int K, int N, int act, int rope_heads, int rope_dim,
                                             float eps);
 
+/* The quantized-weight linears with the residual add that consumes them in
+ * the epilogue: act(a W + bias) rounded to fp16, then fp16(resid + that) --
+ * bit-identical to the plain call followed by add_fp16 (KIND 28: q4_0
+ * blocked along N, the matmul_epilogue_fp16 ABI; KIND 29: q8_0 K-grouped
+ * W^T, as matmul_epilogue_q8k_fp16; KIND 30: q4_0 K-grouped W^T, as
+ * matmul_epilogue_q4k_fp16). resid and out are [M, N]. No reference
+ * counterpart: the fusion of kernels/add_fp16/kernel_api.h into the linear
+ * before it. Each has its plain form's requirements; else a no-op. */
+void matmul_epilogue_res_fp16(const hexlib_hf *a, const unsigned char *w, const float *bias,
+                              const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N, int act);
+void matmul_epilogue_q8k_res_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
+                                  const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N, int act);
+void matmul_epilogue_q4k_res_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
+                                  const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N, int act);
+
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
 int scale_fp16_entry(const hexlib_args *a);
@@ -333,6 +348,9 @@ int layernorm_matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q8k_fp16_entry(const hexlib_args *a);
 int lnfold_matmul_epilogue_f16wt_fp16_entry(const hexlib_args *a);
 int lnfold_matmul_epilogue_f16wt_rope_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_res_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_q8k_res_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_q4k_res_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

@@ -920,3 +920,32 @@ def test_f16wt_harness_cell1_every_path(dev, path):
     assert K.close_f16(got, K.matmul_epilogue_f16w(a, w, bias, act), 0.01, 3e-4).all()
     assert abs(float(got[0, 0]) - 1.1872558) < 1e-3
     assert not K.close_f16(got, NM.epilogue_fp16_accumulation(a, w, bias, act), 0.01, 3e-4).all()
+
+
+@pytest.mark.parametrize("fmt", ["q4n", "q8k", "q4k"])
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 768, 1), (256, 3072, 768, 0), (16, 896, 4864, 0),
+                                        (16, 4864, 896, 2), (1, 768, 256, 1), (4, 896, 4864, 0),
+                                        (70, 512, 96, 1), (300, 1024, 160, 2)])
+def test_quantized_residual_epilogue(dev, fmt, M, Kd, N, act):
+    """KIND 28-30: the quantized linears with the residual add in the
+    epilogue are bit-identical to the plain call followed by add_fp16, on
+    every route the shape takes (one wave per column at M <= 4, the 16-row
+    MFMA form and its split-K reduce at M = 16, the K-across-waves and
+    register-staged kernels above)."""
+    from hexlib_amd.quant import pack_q8_0_kgrouped
+    r = rng(61)
+    a = h16(r.standard_normal((M, Kd)))
+    w = (r.standard_normal((Kd, N)) * 0.02).astype(np.float32)
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    res = h16(r.standard_normal((M, N)))
+    packed = {"q4n": pack_q4_0_nblocked, "q8k": pack_q8_0_kgrouped, "q4k": pack_q4_0_kgrouped}[fmt](w)
+    plain = {"q4n": dev.lib.matmul_epilogue_fp16, "q8k": dev.lib.matmul_epilogue_q8k_fp16,
+             "q4k": dev.lib.matmul_epilogue_q4k_fp16}[fmt]
+    fused = {"q4n": dev.lib.matmul_epilogue_res_fp16, "q8k": dev.lib.matmul_epilogue_q8k_res_fp16,
+             "q4k": dev.lib.matmul_epilogue_q4k_res_fp16}[fmt]
+    da, dw, db, dr = dev.up(a), dev.up(np.frombuffer(packed, np.uint8)), dev.up(bias), dev.up(res)
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    plain(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
+    fused(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr), dev.ptr(d2), M, Kd, N, act)
+    dev.check()
+    np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, dev.down(d1)).view(np.uint16))

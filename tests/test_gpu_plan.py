@@ -98,10 +98,13 @@ def test_qwen_encoder_256_fp16(session):
     assert err <= 2e-2
 
 
-@pytest.mark.parametrize("layout", [None, "q4_0_kgroup"])
-def test_qwen_encoder_reference_q4_config(session, layout):
+@pytest.mark.parametrize("layout,residual", [(None, False), ("q4_0_kgroup", False), (None, True),
+                                             ("q4_0_kgroup", True)])
+def test_qwen_encoder_reference_q4_config(session, layout, residual):
     """The reference's own shipped config: T=2, q4_0 weights. The oracle gets
-    the dequantized, fp16-rounded weights the kernel multiplies with."""
+    the dequantized, fp16-rounded weights the kernel multiplies with. With
+    `residual` the residual adds ride in the q4_0 linears' epilogues (KIND 28
+    blocked along N, KIND 30 grouped along K)."""
     cfg = replace(E.QWEN35_VISION_Q4, depth=2)
     g = E.build_vision_encoder(cfg)
     feeds = E.synthetic_feeds(g, cfg, seed=1)
@@ -114,17 +117,23 @@ def test_qwen_encoder_reference_q4_config(session, layout):
             else:
                 dq = dequantize_q4_0_fp16(pack_q4_0_nblocked(w), w.shape)
             dense[t.name] = np.ascontiguousarray(dq)
-    (out,), _ = _run_plan(session, cfg, feeds, graph_mode=True, weight_layout=layout)
+    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True, weight_layout=layout, residual=residual)
+    if residual:
+        res_spec = "matmul_epilogue_q4k_res" if layout == "q4_0_kgroup" else "matmul_epilogue_res"
+        assert sum(1 for s in wb.op_specs if s == res_spec) == 2 * cfg.depth + 1
     want = _oracle(cfg, feeds, dense)
     err = np.abs(out - want).max()
-    print(f"[qwen q4 {layout}] max abs {err:.3e}", flush=True)
+    print(f"[qwen q4 {layout} residual={residual}] max abs {err:.3e}", flush=True)
     assert err <= 2e-2
 
 
-def test_qwen_encoder_q8_0(session):
-    """cfg 4 with q8_0 weights (KIND 25 for every linear). The oracle gets the
-    dequantized, fp16-rounded weights the kernel multiplies with; the output
-    also stays close to the fp16-weight encoder's (cosine > 0.999)."""
+@pytest.mark.parametrize("residual", [False, True])
+def test_qwen_encoder_q8_0(session, residual):
+    """cfg 4 with q8_0 weights (KIND 25 for every linear; with `residual`
+    KIND 29 for the two residual linears of each block and the patch embed).
+    The oracle gets the dequantized, fp16-rounded weights the kernel
+    multiplies with; the output also stays close to the fp16-weight encoder's
+    (cosine > 0.999)."""
     from hexlib_amd.quant import pack_q8_0_kgrouped
     from oracle.quant import dequantize_q8_0_fp16
     cfg = replace(E.QWEN35_VISION_Q8, depth=4)
@@ -135,8 +144,11 @@ def test_qwen_encoder_q8_0(session):
         if t.dtype == "q8_0":
             w = feeds[t.name]
             dense[t.name] = np.ascontiguousarray(dequantize_q8_0_fp16(pack_q8_0_kgrouped(w), w.shape[::-1]).T)
-    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True)
-    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_q8k") == 6 * cfg.depth + 3
+    (out,), wb = _run_plan(session, cfg, feeds, graph_mode=True, weight_layout="auto" if residual else None,
+                           residual=residual)
+    n_res = 2 * cfg.depth + 1 if residual else 0
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_q8k") == 6 * cfg.depth + 3 - n_res
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_q8k_res") == n_res
     want = _oracle(cfg, feeds, dense)
     err = np.abs(out - want).max()
     cfg16 = replace(cfg, weight_dtype="fp16")

@@ -59,6 +59,10 @@ def test_variant_selection():
     assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q4_0", "fp32"])[0] == "matmul_epilogue"
     assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q4_0", "fp32"],
                   "q4_0_kgroup")[0] == "matmul_epilogue_q4k"
+    assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q4_0", "fp32", "fp16"])[0] == "matmul_epilogue_res"
+    assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q4_0", "fp32", "fp16"],
+                  "q4_0_kgroup")[0] == "matmul_epilogue_q4k_res"
+    assert select("matmul_epilogue", {"act": "none"}, ["fp16", "q8_0", "fp32", "fp16"])[0] == "matmul_epilogue_q8k_res"
     with pytest.raises(SelectError):
         select("softmax", {"axis": 0})
 
@@ -225,8 +229,14 @@ def test_fuse_residual():
     a = eager.run_stored(f, feeds)[g.outputs[0]]
     b = eager.run_stored(r, feeds)[g.outputs[0]]
     np.testing.assert_array_equal(a, b)
+    # quantized weights fold in any layout; fp16 ones only when their layout allows
     q4 = fuse(E.build_vision_encoder(_replace(E.TINY_ENCODER, weight_dtype="q4_0")))
-    assert fuse_residual(q4) is q4
+    rq = fuse_residual(q4, fp16_weights=False)
+    assert len(q4.ops) - len(rq.ops) == 2 * cfg.depth + 1
+    assert fuse_residual(f, fp16_weights=False) is f
+    wbq = WP.build_whole_plan_batch(q4, E.synthetic_feeds(q4, _replace(E.TINY_ENCODER, weight_dtype="q4_0")),
+                                    fuse_first=False, weight_layout=None, residual=True)
+    assert sum(1 for s in wbq.op_specs if s == "matmul_epilogue_res") == 2 * cfg.depth + 1
     cfgq = _replace(E.QWEN35_VISION_FP16, attention="fused_qkv_rope")
     gq = E.build_vision_encoder(cfgq)
     wb = WP.build_whole_plan_batch(gq, E.synthetic_feeds(gq, cfgq), residual=True)
