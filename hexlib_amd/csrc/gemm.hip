@@ -250,6 +250,44 @@ __device__ __forceinline__ void dispatch_epi(int act, bool res, F &&f) {
     }
 }
 
+
+// The plain epilogue of one whole 32x32 block (nb + 32 <= N, 16-byte aligned
+// rows) staged through a wave-private LDS tile (rows of 40 halves): each lane
+// computes its 16 outputs in MFMA order into the tile, then the wave stores
+// the block as 16-byte row segments, four lanes per 64-byte row. Taken by
+// the 64x64 tile, whose four waves each store a block (the folded fc1 at
+// batch 1: 6.67 -> 6.49 us); the 32x32 tile's one storing wave keeps the
+// direct 8-byte stores, which measured faster there.
+template <int ACT, bool RES>
+__device__ __forceinline__ void kw_store_staged_t(const GemmArgs &p, int mb, int nb, int lane, const f32x16 &sum,
+                                                  const BlockBias &bb, const BlockRes &br, f16 *tile) {
+    constexpr int TS = 40;
+    const int r = lane & 31;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        float bv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (lane >> 5) ? bb.v[g * 8 + 4 + e] : bb.v[g * 8 + e];
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(sum[g * 4 + e] + bv[e], br.r[g][e]);
+        *reinterpret_cast<f16x4 *>(tile + r * TS + g * 8 + (lane >> 5) * 4) = o;
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int row = it * 16 + (lane >> 2), c = (lane & 3) * 8;
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(tile + row * TS + c);
+        if (mb + row < p.M) *reinterpret_cast<f16x8 *>(p.C + (long long) (mb + row) * p.ldc + nb + c) = v;
+    }
+}
+
+__device__ __forceinline__ void kw_store_staged(const GemmArgs &p, int mb, int nb, int lane, const f32x16 &sum,
+                                                const BlockBias &bb, const BlockRes &br, f16 *tile) {
+    dispatch_epi(p.act, p.R != nullptr, [&](auto act_c, auto res_c) {
+        kw_store_staged_t<decltype(act_c)::value, decltype(res_c)::value>(p, mb, nb, lane, sum, bb, br, tile);
+    });
+}
+
 __device__ __forceinline__ void kw_store(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
                                          bool vec_store, const BlockBias &bb, const BlockRes &br) {
     const bool res = p.R != nullptr;
@@ -1174,6 +1212,55 @@ __device__ __forceinline__ RopeBlock load_block_rope(const GemmArgs &p, int m, i
     return p.rope_d == 64 ? rope_block_load<64>(p, m, nb, lane) : rope_block_load<0>(p, m, nb, lane);
 }
 
+
+// The rope epilogue of one 32x32 block staged through a wave-private LDS tile
+// (rows of 40 halves) and stored as 16-byte row segments, four lanes per row:
+// the same values as rope_block_store. A rope block (64-wide heads, N % 8,
+// 16-byte aligned rows) holds output features lo0 .. lo0 + 15 and
+// lo0 + 32 .. lo0 + 47 (lo0 = hb + (nb - hb) / 2), staged as one 32-half row;
+// a plain block its 32 columns.
+template <int ACT>
+__device__ __forceinline__ void rope_block_store_staged(const GemmArgs &p, int mb, int nb, int lane,
+                                                        const f32x16 &v, const RopeBlock &rb, f16 *tile) {
+#pragma clang fp contract(off)
+    constexpr int TS = 40;
+    const int r = lane & 31, hi = lane >> 5;
+    const bool rope_blk = nb < p.rope_cols;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if (rope_blk) {
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = f32_rounded(act_t<ACT>(v[g * 4 + e] + rb.bv[g][e]));
+            f16x2 lo, hv;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float x0 = (float) (f16) x[2 * u], x1 = (float) (f16) x[2 * u + 1];
+                const float ca = u ? rb.c0[g].y : rb.c0[g].x, sa = u ? rb.s0[g].y : rb.s0[g].x;
+                const float cb = u ? rb.c1[g].y : rb.c1[g].x, sb = u ? rb.s1[g].y : rb.s1[g].x;
+                const float p0 = x0 * ca, q0 = x1 * sa, p1 = x1 * cb, q1 = x0 * sb;
+                lo[u] = (f16) f32_rounded(p0 - q0);
+                hv[u] = (f16) f32_rounded(p1 + q1);
+            }
+            *reinterpret_cast<f16x2 *>(tile + r * TS + g * 4 + hi * 2) = lo;
+            *reinterpret_cast<f16x2 *>(tile + r * TS + 16 + g * 4 + hi * 2) = hv;
+        } else {
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, false>(v[g * 4 + e] + rb.bv[g][e], (f16) 0);
+            *reinterpret_cast<f16x4 *>(tile + r * TS + g * 8 + hi * 4) = o;
+        }
+    }
+    const int hb = nb & ~63, lo0 = hb + ((nb - hb) >> 1);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int row = it * 16 + (lane >> 2), c = lane & 3;
+        const f16x8 val = *reinterpret_cast<const f16x8 *>(tile + row * TS + c * 8);
+        const int col = rope_blk ? (c < 2 ? lo0 + c * 8 : lo0 + 32 + (c - 2) * 8) : nb + c * 8;
+        if (mb + row < p.M) *reinterpret_cast<f16x8 *>(p.C + (long long) (mb + row) * p.ldc + col) = val;
+    }
+}
+
 __device__ __forceinline__ void store_block_rope(const GemmArgs &p, int m, int nb, int lane, const f32x16 &v,
                                                  const RopeBlock &rb) {
     if (p.act == 1) rope_block_store<1>(p, m, nb, lane, v, rb);
@@ -1492,12 +1579,28 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             for (int e = 0; e < 4; ++e) sum[g * 4 + e] = inv * (sum[g * 4 + e] - mean * lc1[g * 4 + e]);
     }
     if constexpr (ROPE) {   // the rope entry point's guarantees: N % 4, rope_d % 4, ldc == N, no residual
-        store_block_rope(p, m, n0 + (blk % NB) * 32, lane, sum, rblk);
+        const int nb = n0 + (blk % NB) * 32;
+        if (p.rope_d == 64 && p.N % 8 == 0 && nb + 32 <= p.N && (reinterpret_cast<uintptr_t>(p.C) & 15) == 0) {
+            f16 *tile = &sB[1][wave][0];
+            const int mb = m0 + (blk / NB) * 32;
+            if (p.act == 1) rope_block_store_staged<1>(p, mb, nb, lane, sum, rblk, tile);
+            else if (p.act == 2) rope_block_store_staged<2>(p, mb, nb, lane, sum, rblk, tile);
+            else rope_block_store_staged<0>(p, mb, nb, lane, sum, rblk, tile);
+            return;
+        }
+        store_block_rope(p, m, nb, lane, sum, rblk);
         return;
     }
-    if (m >= p.M) return;
     f16 *C = p.C;
     const bool vec_store = (p.ldc & 3) == 0 && hx_aligned8(C) && (!p.R || ((p.ldr & 3) == 0 && hx_aligned8(p.R)));
+    if constexpr (NB == 2) {
+        if (vec_store && (p.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
+            n0 + (blk % NB) * 32 + 32 <= p.N) {
+            kw_store_staged(p, m0 + (blk / NB) * 32, n0 + (blk % NB) * 32, lane, sum, bbias, bres, &sB[1][wave][0]);
+            return;
+        }
+    }
+    if (m >= p.M) return;
     kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store, bbias, bres);
 }
 
