@@ -1299,8 +1299,9 @@ __device__ __forceinline__ void load_block_c1(const GemmArgs &p, int nb, int lan
 template <int T, bool ROPE = false, bool KN = false, int QB = 0, bool LNF = false>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
-    static_assert(QB == 0 || (!ROPE && (QB == 8 || QB == 4) && (!KN || QB == 4)),
-                  "quantized weights: q8_0 / q4_0 blocks along K of W^T, or q4_0 blocks along N of [K][N]");
+    static_assert(QB == 0 || ((QB == 8 || QB == 4) && (!KN || QB == 4) && (!ROPE || (QB == 8 && !KN))),
+                  "quantized weights: q8_0 / q4_0 blocks along K of W^T, or q4_0 blocks along N of [K][N]; "
+                  "the rope epilogue with q8_0 blocks along K (rows pair-interleaved like the fp16 W^T)");
     static_assert(!LNF || (T == 64 && !KN && QB == 0), "the folded LayerNorm takes the 64x64 W^T form");
     constexpr bool Q8 = QB != 0;                 // a block-quantized weight (either format)
     constexpr int QBYTES = QB == 8 ? 34 : 18;
@@ -2986,6 +2987,28 @@ extern "C" void matmul_epilogue_q4k_fp16(const hexlib_hf *a, const unsigned char
     if (!hx::aligned(wt, 2)) return;
     launch<B_Q4K>(args(a, K, 0, wt, (long long) (K / 32) * 18, 0, bias, out, N, 0, M, N, K, act), 1,
                   K % 8 == 0 && hx::aligned(a, 16), false);
+}
+
+// The q8_0 (K-grouped W^T) form of matmul_epilogue_f16wt_rope_fp16: the rows
+// of W^T pair-interleaved within each rope head before quantization (rows are
+// quantized independently, so that is the same blocks as the original rows,
+// reordered), dequantized into the K-across-waves kernel's ring; the rope
+// epilogue as the fp16 form's. Requires K % 256 == 0.
+extern "C" void matmul_epilogue_q8k_rope_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
+                                              const float *costab, const float *sintab, hexlib_hf *out, int M,
+                                              int K, int N, int act, int rope_heads, int rope_dim) {
+    if (!a || !wt || !out || !costab || !sintab || !dims_ok(M, K, N, 1) || act < 0 || act > 2) return;
+    const long long rope_cols = 2LL * rope_heads * rope_dim;
+    if (rope_heads <= 0 || rope_dim <= 0 || rope_dim % 4 || rope_cols > N || N % 4 || K % KW_BK ||
+        !hx::aligned(a, 16) || !hx::aligned(wt, 2) || !hx::aligned(out, 8))
+        return;
+    GemmArgs p = args(a, K, 0, wt, (long long) (K / 32) * 34, 0, bias, out, N, 0, M, N, K, act);
+    p.rcos = costab;
+    p.rsin = sintab;
+    p.rope_cols = (int) rope_cols;
+    p.rope_d = rope_dim;
+    const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
+    HX_LAUNCH((gemm_nk_kw<64, true, false, 8>), grid, dim3(TPB), 0, p);
 }
 
 // The quantized-weight linears with the residual add that consumes them in

@@ -59,6 +59,7 @@ KIND_ID: dict[str, int] = {
     "matmul_epilogue_res": 28,
     "matmul_epilogue_q8k_res": 29,
     "matmul_epilogue_q4k_res": 30,
+    "matmul_epilogue_q8k_rope": 31,
 }
 
 
@@ -351,6 +352,18 @@ SPECS: dict[str, RunnerSpec] = {
         weight=(3, "fp16"), rank=2,
         notes="extension: layernorm over K then the W^T linear, one launch "
               "(fused by hexlib_amd.graph.fuse.fuse_layernorm)"),
+    "matmul_epilogue_q8k_rope": RunnerSpec(
+        "matmul_epilogue", "matmul_epilogue_q8k_rope_fp16", ("fp16", "q8_0", "fp32", "fp32", "fp32"), "fp16",
+        _MM_SCALARS + (_S("attr:rope_heads", "rope_heads"), _S("attr:rope_dim", "rope_dim")),
+        layouts=("row_major", "q8_0_kgroup_rope", "row_major", "col_major", "col_major", "row_major"),
+        extents=("(uint64_t)M*K", "(uint64_t)K*N", "N", "(uint64_t)M*rope_dim", "(uint64_t)M*rope_dim",
+                 "(uint64_t)M*N"),
+        checks=("K % 256 == 0", "N % 4 == 0", "rope_dim % 4 == 0", "2LL * rope_heads * rope_dim <= N",
+                "((uintptr_t)a->buf[0] & 15) == 0", "((uintptr_t)a->buf[1] & 1) == 0",
+                "((uintptr_t)a->buf[5] & 7) == 0"),
+        weight=(1, "q8_0"), primary=False, rank=2,
+        notes="extension: the fused q/k/v linear with q8_0 weights and rope_2d on its q and k heads in "
+              "the epilogue (fuse_rope)"),
     "lnfold_matmul_epilogue_f16wt": RunnerSpec(
         "lnfold_matmul_epilogue", "lnfold_matmul_epilogue_f16wt_fp16", ("fp16", "fp16", "fp32"), "fp16",
         _MM_SCALARS + (_S("attr:eps", "eps", "float"),),

@@ -92,6 +92,25 @@ def stage_col_major_rope(w, heads: int, d: int) -> bytes:
     return wt.tobytes()
 
 
+def rope_row_order(n: int, heads: int, d: int) -> np.ndarray:
+    """The col_major_rope row order of an N-row W^T: within each of the first
+    `2 * heads` heads of `d`, stored row 2i is feature i and row 2i + 1 is
+    feature i + d/2; rows past them stay in place."""
+    i = np.arange(d)
+    src = np.where(i % 2 == 0, i // 2, i // 2 + d // 2)
+    order = np.arange(n)
+    order[:2 * heads * d] = (np.arange(2 * heads)[:, None] * d + src[None, :]).reshape(-1)
+    return order
+
+
+def stage_q8_0_kgroup_rope(w, heads: int, d: int) -> bytes:
+    """A `[K, N]` weight in the `q8_0_kgroup_rope` layout: the q8_0 blocks
+    along K of W^T in the col_major_rope row order. Rows are quantized one by
+    one, so these are the q8_0_kgroup blocks of the same rows, reordered."""
+    w = np.asarray(w, dtype=np.float32)
+    return pack_q8_0_kgrouped(np.ascontiguousarray(w[:, rope_row_order(w.shape[1], heads, d)]))
+
+
 def _spec_for(op, graph: Graph, weight_layout: str | None) -> tuple[str, RunnerSpec]:
     """`weight_layout="auto"` stores fp16 weights transposed (col_major: both
     GEMM operands K-contiguous, the fast path) and q4_0 weights in the
@@ -213,9 +232,10 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
             continue
         name, spec = _spec_for(op, g, weight_layout)
         op_specs[op.id] = (name, spec)
-        if "col_major_rope" in spec.buf_layouts():
-            claim(rope_of, op.inputs[spec.buf_layouts().index("col_major_rope")],
-                  (int(op.attrs["rope_heads"]), int(op.attrs["rope_dim"])), f"op {op.id} rope")
+        for rope_layout in ("col_major_rope", "q8_0_kgroup_rope"):
+            if rope_layout in spec.buf_layouts():
+                claim(rope_of, op.inputs[spec.buf_layouts().index(rope_layout)],
+                      (int(op.attrs["rope_heads"]), int(op.attrs["rope_dim"])), f"op {op.id} rope")
         lays = spec.buf_layouts()
         for i, n in enumerate(op.inputs):
             claim(layout_of, n, lays[i], f"op {op.id} src{i}")
@@ -281,6 +301,8 @@ def build_whole_plan_batch(graph: Graph, feeds: Mapping[str, Any],
                 data = pack_q4_0_kgrouped(np.asarray(value))
             elif p.layout == "q8_0_kgroup":
                 data = pack_q8_0_kgrouped(np.asarray(value))
+            elif p.layout == "q8_0_kgroup_rope":
+                data = stage_q8_0_kgroup_rope(value, *rope_of[n])
             else:
                 data = pack_q4_0_nblocked(np.asarray(value))
         elif p.layout == "col_major_rope":

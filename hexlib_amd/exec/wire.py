@@ -36,10 +36,11 @@ STATUS_NAME = {v: k for k, v in STATUS.items()}
 # `q4_0_kgroup` (q4_0 blocks along K of W^T), `col_major` (a [K, N] weight
 # stored as W^T [N, K]) and `col_major_rope` (col_major with the rows of each
 # rope head pair-interleaved: row 2i = feature i, row 2i + 1 = feature i + D/2)
-# and `q8_0_kgroup` (q8_0 blocks along K of W^T).
+# and `q8_0_kgroup` (q8_0 blocks along K of W^T), `q8_0_kgroup_rope`
+# (q8_0_kgroup of the col_major_rope row order).
 DTYPE_ID = {"fp32": 0, "fp16": 1, "q4_0": 2, "int32": 3, "q8_0": 4}
 LAYOUT_ID = {"row_major": 0, "tiled_32x32": 1, "q4_0_repacked": 2, "q4_0_kgroup": 3,
-             "col_major": 4, "col_major_rope": 5, "q8_0_kgroup": 6}
+             "col_major": 4, "col_major_rope": 5, "q8_0_kgroup": 6, "q8_0_kgroup_rope": 7}
 
 _HDR = "<10I"
 _BUF = "<QQII"

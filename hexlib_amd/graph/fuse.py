@@ -151,7 +151,9 @@ def fuse_rope(graph: Graph) -> Graph:
         mm = producer.get(shp.inputs[0])
         if mm is None or mm.kind != "matmul_epilogue" or len(mm.inputs) != 3:
             continue
-        if graph.tensor(mm.inputs[1]).dtype != "fp16" or shp.inputs[0] in outputs:
+        # fp16 weights (staged col_major_rope) and q8_0 ones (K-grouped blocks of
+        # the same row order); q4_0 has no rope kernel
+        if graph.tensor(mm.inputs[1]).dtype not in ("fp16", "q8_0") or shp.inputs[0] in outputs:
             continue
         if len(readers.get(shp.inputs[0], [])) != 1 or len(readers.get(qk, [])) != 1:
             continue

@@ -43,6 +43,7 @@ SIGNATURES = {
     "matmul_epilogue_res_fp16": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_q8k_res_fp16": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "matmul_epilogue_q4k_res_fp16": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    "matmul_epilogue_q8k_rope_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "matmul_epilogue_f16wt_rope_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "attention_qkv_fp16": (None, [_P, _P, _I, _I, _I, _I, _F]),
     "layernorm_matmul_epilogue_f16wt_fp16": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F]),

@@ -77,6 +77,7 @@ enum hexlib_dsp_status {
 #define HEXLIB_LAYOUT_COL_MAJOR     4u
 #define HEXLIB_LAYOUT_COL_MAJOR_ROPE 5u
 #define HEXLIB_LAYOUT_Q8_0_KGROUP   6u
+#define HEXLIB_LAYOUT_Q8_0_KGROUP_ROPE 7u
 
 /* Dtype ids: hexlib/runtime/wire.py:61. */
 #define HEXLIB_DTYPE_FP32  0u
@@ -321,6 +322,16 @@ void matmul_epilogue_q8k_res_fp16(const hexlib_hf *a, const unsigned char *wt, c
 void matmul_epilogue_q4k_res_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
                                   const hexlib_hf *resid, hexlib_hf *out, int M, int K, int N, int act);
 
+/* matmul_epilogue_f16wt_rope_fp16 with a q8_0 weight (KIND 31): wt holds
+ * the K-grouped q8_0 blocks of W^T whose rows are pair-interleaved within
+ * each of the first 2 * rope_heads heads (layout 7, q8_0_kgroup_rope: the
+ * col_major_rope row order, then quantized row by row). Requires K % 256 == 0
+ * and the rope entry's conditions; else a no-op. No reference counterpart:
+ * the fusion of kernels/rope_2d_fp16/kernel_api.h into the q8_0 linear. */
+void matmul_epilogue_q8k_rope_fp16(const hexlib_hf *a, const unsigned char *wt, const float *bias,
+                                   const float *costab, const float *sintab, hexlib_hf *out, int M, int K,
+                                   int N, int act, int rope_heads, int rope_dim);
+
 /* ---- 2. entry adapters (generated) ---- */
 int add_fp16_entry(const hexlib_args *a);
 int scale_fp16_entry(const hexlib_args *a);
@@ -351,6 +362,7 @@ int lnfold_matmul_epilogue_f16wt_rope_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_res_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q8k_res_fp16_entry(const hexlib_args *a);
 int matmul_epilogue_q4k_res_fp16_entry(const hexlib_args *a);
+int matmul_epilogue_q8k_rope_fp16_entry(const hexlib_args *a);
 
 /* ---- library control ---- */
 /* The stream every per-kernel call enqueues on (a hipStream_t; NULL = the

@@ -949,3 +949,40 @@ def test_quantized_residual_epilogue(dev, fmt, M, Kd, N, act):
     fused(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(dr), dev.ptr(d2), M, Kd, N, act)
     dev.check()
     np.testing.assert_array_equal(dev.down(d2).view(np.uint16), K.add_fp16(res, dev.down(d1)).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,Kd,heads,d,extra", [(256, 768, 12, 64, 768), (70, 512, 2, 64, 128), (200, 256, 3, 16, 32)])
+def test_q8k_rope_epilogue(dev, M, Kd, heads, d, extra):
+    """KIND 31: the q8_0 weight in the q8_0_kgroup_rope layout (W^T rows in the
+    col_major_rope order, quantized row by row) on the K-across-waves kernel
+    with the rope epilogue is bit-identical to the fp16 rope linear (the same
+    64x64 K-across-waves tile) on the weight it dequantizes to."""
+    from hexlib_amd.exec.wholeplan import rope_row_order, stage_q8_0_kgroup_rope
+    from oracle.quant import dequantize_q8_0_fp16
+    r = rng(62)
+    N = 2 * heads * d + extra
+    a = h16(r.standard_normal((M, Kd)))
+    w = (r.standard_normal((Kd, N)) * 0.02).astype(np.float32)
+    bias = (0.05 * r.standard_normal(N)).astype(np.float32)
+    cos, sin = _rope_tables(r, M, d)
+    wq = stage_q8_0_kgroup_rope(w, heads, d)
+    # the fp16 W^T it dequantizes to, already in the col_major_rope row order
+    wt16 = h16(dequantize_q8_0_fp16(wq, (N, Kd)))
+    da, db, dq, dw16 = dev.up(a), dev.up(bias), dev.up(np.frombuffer(wq, np.uint8)), dev.up(np.ascontiguousarray(wt16))
+    dc, ds = dev.up(np.ascontiguousarray(cos.T)), dev.up(np.ascontiguousarray(sin.T))
+    d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
+    assert dev.lib.hexlib_gpu_gemm_override(64, 64, 0, 4) == 1
+    try:
+        dev.lib.matmul_epilogue_f16wt_rope_fp16(dev.ptr(da), dev.ptr(dw16), dev.ptr(db), dev.ptr(dc), dev.ptr(ds),
+                                                dev.ptr(d1), M, Kd, N, 0, heads, d)
+        dev.check()
+    finally:
+        dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
+    dev.lib.matmul_epilogue_q8k_rope_fp16(dev.ptr(da), dev.ptr(dq), dev.ptr(db), dev.ptr(dc), dev.ptr(ds),
+                                          dev.ptr(d2), M, Kd, N, 0, heads, d)
+    dev.check()
+    np.testing.assert_array_equal(dev.down(d2).view(np.uint16), dev.down(d1).view(np.uint16))
+    # and the rows really are the original weight's, reordered
+    from hexlib_amd.quant import pack_q8_0_kgrouped
+    w16_orig = h16(dequantize_q8_0_fp16(pack_q8_0_kgrouped(w), (N, Kd)))
+    np.testing.assert_array_equal(wt16, w16_orig[rope_row_order(N, heads, d)])

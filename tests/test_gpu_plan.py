@@ -127,6 +127,32 @@ def test_qwen_encoder_reference_q4_config(session, layout, residual):
     assert err <= 2e-2
 
 
+def test_qwen_encoder_q8_0_fused(session):
+    """The bench's q8_0 plan: fused q/k/v with the q/k rope in the q8_0 GEMM's
+    epilogue (KIND 31, attention reading its output), the residual adds in
+    the q8_0 linears' epilogues (KIND 29): against the storage-rounding oracle
+    of the REFERENCE graph on the dequantized weights, <= 2e-2 max abs."""
+    from hexlib_amd.quant import pack_q8_0_kgrouped
+    from oracle.quant import dequantize_q8_0_fp16
+    cfg_ref = replace(E.QWEN35_VISION_Q8, depth=4)
+    g_ref = E.build_vision_encoder(cfg_ref)
+    feeds = E.synthetic_feeds(g_ref, cfg_ref, seed=2)
+    dense = {}
+    for t in g_ref.tensors.values():
+        if t.dtype == "q8_0":
+            w = feeds[t.name]
+            dense[t.name] = np.ascontiguousarray(dequantize_q8_0_fp16(pack_q8_0_kgrouped(w), w.shape[::-1]).T)
+    cfg = replace(cfg_ref, attention="fused_qkv_rope")
+    (out,), wb = _run_plan(session, cfg, E.fuse_qkv_feeds(feeds, cfg), graph_mode=True, weight_layout="auto",
+                           residual=True, rope=True)
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_q8k_rope") == cfg.depth
+    assert sum(1 for s in wb.op_specs if s == "matmul_epilogue_q8k_res") == 2 * cfg.depth + 1
+    want = _oracle(cfg_ref, feeds, dense)
+    err = np.abs(out - want).max()
+    print(f"[qwen q8_0 fused] max abs vs reference graph {err:.3e}", flush=True)
+    assert err <= 2e-2
+
+
 @pytest.mark.parametrize("residual", [False, True])
 def test_qwen_encoder_q8_0(session, residual):
     """cfg 4 with q8_0 weights (KIND 25 for every linear; with `residual`
