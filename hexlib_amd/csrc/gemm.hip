@@ -775,7 +775,13 @@ __device__ __forceinline__ f16x8 kn_frag(const f16 *bs, int ncol, int q, int lan
 // streams through the ring (BM = 64, K <= 64 * LN_KT, 512 <= K).
 // KN: the weight is [K][N] (matmul_fp16, matmul_epilogue_f16w), copied into
 // the ring as stored (N % 64 == 0) and read through kn_frag.
-template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false, bool LN = false, bool KN = false>
+// LNF (the 64x64 pipelined form only, one split): a LayerNorm over A's rows
+// folded into the product as gemm_nk_kw's LNF form does it -- bias holds
+// [c2 | c1]; the two waves of a wave row read the same A fragments, so wave
+// column 0 sums x and column 1 sums x^2 (v_dot2_f32_f16); the sums meet in
+// LDS after the loop and the epilogue applies rstd (acc - mean c1).
+template <int BM, int BN, int STAGES, int WM = 2, int WN = 2, bool ROPE = false, bool LN = false, bool KN = false,
+          bool LNF = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     constexpr int NW = WM * WN;
     constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
@@ -786,8 +792,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     // one 32x32 block per wave: the software-pipelined loop (see below)
     constexpr bool PIPE = TM == 1 && TN == 1 && !LN;
     static_assert(!PIPE || LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
+    static_assert(!LNF || (PIPE && WN == 2 && !KN), "the folded LayerNorm takes the pipelined 2x2-wave form");
     __shared__ __attribute__((aligned(16))) f16 sA[LN ? LN_KT : STAGES][BM * DS_ROW];
     __shared__ __attribute__((aligned(16))) f16 sB[STAGES][BN * DS_ROW];
+    // LNF: sum x (wave column 0) and sum x^2 (column 1) per [tile row][lane / 32]
+    __shared__ float2 lnf_sums[LNF ? BM * 2 : 1];
+    float lnf_acc = 0.0f;
 
     const int bz = blockIdx.z / p.splits;
     const int split = blockIdx.z % p.splits;
@@ -810,12 +820,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
     // hidden (one column block per wave only: more would cost occupancy).
     constexpr bool BIAS_EARLY = TN == 1 && !ROPE;
     float bearly[BIAS_EARLY ? 4 : 1][4];
+    float c1early[BIAS_EARLY && LNF ? 4 : 1][4];   // LNF: c1 (bias + N) likewise
     if constexpr (BIAS_EARLY) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int n = n0 + wn + g * 8 + (lane >> 5) * 4;
 #pragma unroll
             for (int e = 0; e < 4; ++e) bearly[g][e] = (p.bias && p.splits == 1 && n + e < p.N) ? p.bias[n + e] : 0.0f;
+            if constexpr (LNF) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) c1early[g][e] = n + e < p.N ? p.bias[p.N + n + e] : 0.0f;
+            }
         }
     }
 
@@ -878,6 +893,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
 #pragma unroll
             for (int q = 0; q < BK / 16; ++q)
                 acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.w[q], cur.x[q], acc[0][0], 0, 0, 0);
+            if constexpr (LNF) {
+                const f16x2 one2 = {(f16) 1.0f, (f16) 1.0f};
+                const bool sq = __builtin_amdgcn_readfirstlane(wave % WN) != 0;
+#pragma unroll
+                for (int q = 0; q < BK / 16; ++q)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f16x2 pr = {cur.x[q][2 * u], cur.x[q][2 * u + 1]};
+                        lnf_acc = __builtin_amdgcn_fdot2(pr, sq ? pr : one2, lnf_acc, false);
+                    }
+            }
             __builtin_amdgcn_sched_barrier(0);
             if (kt + 1 < KT) {
                 // slice kt + 1 is complete for this wave once at most the slices
@@ -980,6 +1006,31 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
         return;
     }
     f16 *C = p.C + (long long) bz * p.sC;
+    // LNF: this lane's row (wm + lane % 32) mean and rstd, from the two wave
+    // columns' sums of both lane halves, in a fixed order
+    float lnf_mean = 0.0f, lnf_inv = 1.0f;
+    if constexpr (LNF) {
+        const int ra = wm + (lane & 31);
+        reinterpret_cast<float *>(lnf_sums)[(ra * 2 + (lane >> 5)) * 2 + wave % WN] = lnf_acc;
+        HX_WAIT_LGKM0();
+        __builtin_amdgcn_s_barrier();
+        const float2 a = lnf_sums[ra * 2], b = lnf_sums[ra * 2 + 1];
+        lnf_mean = (a.x + b.x) / (float) p.K;
+        const float var = fmaxf((a.y + b.y) / (float) p.K - lnf_mean * lnf_mean, 0.0f);
+        lnf_inv = 1.0f / sqrtf(var + p.lnf_eps);
+    }
+    // the value of accumulator element e of group g (column n + e; f: the bias
+    // index, the output feature) after the folded LayerNorm's correction
+    auto lnf = [&](float v, int f) {
+        if constexpr (LNF) return lnf_inv * (v - lnf_mean * p.bias[p.N + f]);
+        else return v;
+    };
+    // the plain epilogue's: group g, element e of column n + e (c1 prefetched
+    // with the bias where it was)
+    auto lnf_plain = [&](float v, int g, int e, int n) {
+        if constexpr (LNF && BIAS_EARLY) return lnf_inv * (v - lnf_mean * c1early[g][e]);
+        else return lnf(v, n + e);
+    };
     if constexpr (ROPE) {
         // the rope entry point guarantees N % 4 == 0, rope_d % 4 == 0, ldc == N,
         // an 8-byte aligned C, one batch and no residual: every group
@@ -1031,16 +1082,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
                         const int m = m0 + wm + i * 32 + (lane & 31);
                         if (m >= p.M) continue;
                         f16 *crow = C + (long long) m * p.ldc;
+                        const int f[4] = {q[h].lo, rope[h] ? q[h].hi : n + 1, q[h].lo + (rope[h] ? 1 : 2),
+                                          rope[h] ? q[h].hi + 1 : n + 3};
                         if (rope[h]) {
                             float v[4];
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) v[e] = f32_rounded(act_t<ACT>(acc[j][i][g * 4 + e] + bv[h][e]));
+                            for (int e = 0; e < 4; ++e)
+                                v[e] = f32_rounded(act_t<ACT>(lnf(acc[j][i][g * 4 + e], f[e]) + bv[h][e]));
                             rope_store4(crow, q[h], v, c0[h][i], c1[h][i], s0[h][i], s1[h][i]);
                         } else {
                             f16x4 o;
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
-                                o[e] = epi_t<ACT, false>(acc[j][i][g * 4 + e] + bv[h][e], (f16) 0);
+                                o[e] = epi_t<ACT, false>(lnf(acc[j][i][g * 4 + e], f[e]) + bv[h][e], (f16) 0);
                             *reinterpret_cast<f16x4 *>(crow + n) = o;
                         }
                     }
@@ -1072,12 +1126,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nk_lds(GemmArgs p) {
                     const f16x4 r4 = RES ? *reinterpret_cast<const f16x4 *>(p.R + m * p.ldr + n) : f16x4{};
                     f16x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(acc[j][i][g * 4 + e] + bv[e], r4[e]);
+                    for (int e = 0; e < 4; ++e) o[e] = epi_t<ACT, RES>(lnf_plain(acc[j][i][g * 4 + e], g, e, n) + bv[e], r4[e]);
                     *reinterpret_cast<f16x4 *>(dst) = o;
                 } else {
-                    store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr,
-                               acc[j][i][g * 4] + bv[0], acc[j][i][g * 4 + 1] + bv[1],
-                               acc[j][i][g * 4 + 2] + bv[2], acc[j][i][g * 4 + 3] + bv[3]);
+                    float t[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = n + e < p.N ? lnf_plain(acc[j][i][g * 4 + e], g, e, n) + bv[e] : 0.0f;
+                    store_tail(dst, p.N - n, p.act, p.R ? p.R + m * p.ldr + n : nullptr, t[0], t[1], t[2], t[3]);
                 }
             }
         }
@@ -2914,12 +2969,26 @@ static bool launch_big_lnf(const GemmArgs &p) {
     return true;
 }
 
+// Between the two: where the K-across-waves form's 64x64 tiles (one workgroup
+// per CU) need more than a round of CUs, the tiled 64x64 form (two per CU),
+// as the unfolded linear takes it there (448x448 at batch 1: 784 rows).
+static bool launch_lds_lnf(const GemmArgs &p) {
+    const long long tiles = (long long) ((p.M + 63) / 64) * ((p.N + 63) / 64);
+    if (tiles <= 256) return false;
+    const dim3 grid((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64), 1);
+    if (p.rcos) HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, true, false, false, true>), grid, dim3(TPB), 0, p);
+    else HX_LAUNCH((gemm_nk_lds<64, 64, 4, 2, 2, false, false, false, true>), grid, dim3(TPB), 0, p);
+    return true;
+}
+
 extern "C" void lnfold_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const hexlib_hf *wt, const float *bias2,
                                                   hexlib_hf *out, int M, int K, int N, int act, float eps) {
     if (!lnf_ok(x, wt, bias2, out, M, K, N, act)) return;
     GemmArgs p = args(x, K, 0, wt, K, 0, bias2, out, N, 0, M, N, K, act);
     p.lnf_eps = eps;
-    if (launch_big_lnf(p)) return;
+    p.splits = 1;
+    p.k_per_split = K;
+    if (launch_big_lnf(p) || launch_lds_lnf(p)) return;
     const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
     HX_LAUNCH((gemm_nk_kw<64, false, false, 0, true>), grid, dim3(TPB), 0, p);
 }
@@ -2937,7 +3006,9 @@ extern "C" void lnfold_matmul_epilogue_f16wt_rope_fp16(const hexlib_hf *x, const
     p.rope_cols = (int) rope_cols;
     p.rope_d = rope_dim;
     p.lnf_eps = eps;
-    if (launch_big_lnf(p)) return;
+    p.splits = 1;
+    p.k_per_split = K;
+    if (launch_big_lnf(p) || launch_lds_lnf(p)) return;
     const dim3 grid((unsigned) ((N + 63) / 64), (unsigned) ((M + 63) / 64));
     HX_LAUNCH((gemm_nk_kw<64, true, false, 0, true>), grid, dim3(TPB), 0, p);
 }

@@ -290,8 +290,9 @@ void layernorm_matmul_epilogue_f16wt_fp16(const hexlib_hf *x, const float *ln_w,
  * transposed; bias2 holds 2N floats: c2[n] = bias[n] + sum_k ln_b[k] W[k][n],
  * then c1[n] = sum_k W'[k][n]. out = act(rstd (x W' - mean c1) + c2), with
  * each row's mean and one-pass variance taken in fp32 from the x tiles the
- * product reads (the K-across-waves kernel at few rows, the large-tile kernel
- * where its 128-row tiles fill the GPU). Within the GEMM tolerance of
+ * product reads (the K-across-waves kernel at few rows, the tiled 64x64
+ * kernel above a round of its tiles, the large-tile kernel where its 128-row
+ * tiles fill the GPU). Within the GEMM tolerance of
  * layernorm_fp16 followed by matmul_epilogue_f16wt_fp16, not bit-identical
  * to them. No reference counterpart: the fusion of
  * kernels/layernorm_fp16/kernel_api.h:38-39 into the linear that consumes

@@ -95,11 +95,14 @@ def _inputs(seed, M, Kd, N, offset=0.5, scale=2.0):
 @pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 3072, 1), (256, 768, 2304, 0), (200, 512, 200, 2),
                                         (65, 256, 64, 1), (1, 768, 96, 0), (784, 768, 3072, 1),
                                         (256, 1024, 136, 0),
+                                        # the tiled 64x64 form (more 64x64 tiles than CUs; ragged N)
+                                        (1000, 256, 1100, 2),
                                         # the large-tile form: 128 x 192 tiles (ragged M), 128 x 128
                                         (4160, 768, 1536, 1), (8192, 768, 3072, 1), (8192, 512, 512, 0)])
 def test_lnfold_linear(dev, M, Kd, N, act):
-    """KIND 26 on the K-across-waves form (few rows) and the large-tile form
-    (tiles filling a round of CUs)."""
+    """KIND 26 on the K-across-waves form (its 64x64 tiles within a round of
+    CUs), the tiled 64x64 form (784 rows: 448x448) and the large-tile form
+    (128-row tiles filling a round of CUs)."""
     x, g, b, w, bias = _inputs(41, M, Kd, N)
     wt = np.ascontiguousarray(lnfold_weight(w, g).T)
     b2 = lnfold_bias2(w, g, b, bias)
@@ -140,6 +143,8 @@ def _rope_tables(r, M, d):
 
 @pytest.mark.parametrize("M,Kd,heads,d,extra", [(256, 768, 12, 64, 768), (70, 256, 2, 64, 128),
                                                 (200, 512, 3, 16, 32),
+                                                # the tiled 64x64 rope form
+                                                (784, 768, 12, 64, 768), (1000, 256, 8, 16, 1088),
                                                 # the large-tile rope forms: 128 x 192, 128 x 128
                                                 (8192, 768, 12, 64, 768), (8192, 256, 3, 64, 128)])
 def test_lnfold_rope_linear(dev, M, Kd, heads, d, extra):
