@@ -196,10 +196,11 @@ struct BlockRes {
     f16x4 r[4];
 };
 
+template <int NG = 4>
 __device__ __forceinline__ BlockRes load_block_res(const GemmArgs &p, int m, int nb, int lane, bool vec_store) {
-    BlockRes t;
+    BlockRes t{};
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < NG; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
         t.r[g] = p.R && vec_store && m < p.M && n + 3 < p.N
                      ? *reinterpret_cast<const f16x4 *>(p.R + (long long) m * p.ldr + n) : f16x4{};
@@ -207,11 +208,12 @@ __device__ __forceinline__ BlockRes load_block_res(const GemmArgs &p, int m, int
     return t;
 }
 
-template <int ACT, bool RES>
+// NG: the 8-column groups stored (3: the first 24 columns of a 32 x 24 tile).
+template <int ACT, bool RES, int NG = 4>
 __device__ __forceinline__ void kw_store_t(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
                                            bool vec_store, const BlockBias &bb, const BlockRes &br) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < NG; ++g) {
         const int n = nb + g * 8 + (lane >> 5) * 4;
         float bv[4];
 #pragma unroll
@@ -288,18 +290,19 @@ __device__ __forceinline__ void kw_store_staged(const GemmArgs &p, int mb, int n
     });
 }
 
+template <int NG = 4>
 __device__ __forceinline__ void kw_store(const GemmArgs &p, int m, int nb, int lane, const f32x16 &sum,
                                          bool vec_store, const BlockBias &bb, const BlockRes &br) {
     const bool res = p.R != nullptr;
     if (p.act == 1) {
-        if (res) kw_store_t<1, true>(p, m, nb, lane, sum, vec_store, bb, br);
-        else kw_store_t<1, false>(p, m, nb, lane, sum, vec_store, bb, br);
+        if (res) kw_store_t<1, true, NG>(p, m, nb, lane, sum, vec_store, bb, br);
+        else kw_store_t<1, false, NG>(p, m, nb, lane, sum, vec_store, bb, br);
     } else if (p.act == 2) {
-        if (res) kw_store_t<2, true>(p, m, nb, lane, sum, vec_store, bb, br);
-        else kw_store_t<2, false>(p, m, nb, lane, sum, vec_store, bb, br);
+        if (res) kw_store_t<2, true, NG>(p, m, nb, lane, sum, vec_store, bb, br);
+        else kw_store_t<2, false, NG>(p, m, nb, lane, sum, vec_store, bb, br);
     } else {
-        if (res) kw_store_t<0, true>(p, m, nb, lane, sum, vec_store, bb, br);
-        else kw_store_t<0, false>(p, m, nb, lane, sum, vec_store, bb, br);
+        if (res) kw_store_t<0, true, NG>(p, m, nb, lane, sum, vec_store, bb, br);
+        else kw_store_t<0, false, NG>(p, m, nb, lane, sum, vec_store, bb, br);
     }
 }
 
@@ -1351,13 +1354,21 @@ __device__ __forceinline__ void load_block_c1(const GemmArgs &p, int nb, int lan
 // exact in fp32). The four waves' sums give the row's mean and one-pass
 // variance in fp32 after the loop; the epilogue applies
 // rstd (acc - mean c1[n]) before the bias (c2) and the activation.
-template <int T, bool ROPE = false, bool KN = false, int QB = 0, bool LNF = false>
+// TN: the tile's output columns -- T, or 24 with T = 32 (plain fp16 W^T only):
+// the MFMAs keep their 32 columns, the last 8 multiplying copies of the tile's
+// row 23 of W^T (the copy clamps there), and the epilogue stores 24. Where
+// 32 x 32 tiles leave CUs idle (N = 768 at 256 rows: 192 tiles) 32 x 24 fills
+// a round of 256 with 12.5% fewer bytes per workgroup.
+template <int T, bool ROPE = false, bool KN = false, int QB = 0, bool LNF = false, int TN = T>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
     static_assert(QB == 0 || ((QB == 8 || QB == 4) && (!KN || QB == 4) && (!ROPE || (QB == 8 && !KN))),
                   "quantized weights: q8_0 / q4_0 blocks along K of W^T, or q4_0 blocks along N of [K][N]; "
                   "the rope epilogue with q8_0 blocks along K (rows pair-interleaved like the fp16 W^T)");
     static_assert(!LNF || (T == 64 && !KN && QB == 0), "the folded LayerNorm takes the 64x64 W^T form");
+    static_assert(TN == T || (T == 32 && TN == 24 && !ROPE && !KN && QB == 0 && !LNF),
+                  "the 32 x 24 tile: plain fp16 W^T");
+    constexpr int NG = TN == T ? 4 : TN / 8;   // 8-column groups stored per 32-column block
     constexpr bool Q8 = QB != 0;                 // a block-quantized weight (either format)
     constexpr int QBYTES = QB == 8 ? 34 : 18;
     constexpr int NB = T / 32;                 // 32-row blocks per tile side
@@ -1369,9 +1380,10 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) f16 sB[STAGES][4][T * DS_ROW];
     const f16 *A = p.A;
     const f16 *B = reinterpret_cast<const f16 *>(p.B);
-    const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
+    const int m0 = blockIdx.y * T, n0 = blockIdx.x * TN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int KT = p.K / KW_BK;
+    const int nrows = TN == T ? p.N : min(p.N, n0 + TN);   // W^T rows copied, the rest clamped to the last
 
     auto issue = [&](int kt, int st) {
 #pragma unroll
@@ -1379,7 +1391,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
             lds_copy_slice<T, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
             if constexpr (Q8) continue;
             else if constexpr (KN) lds_copy_slice<64, 4>(B, p.ldb, kt * KW_BK + sub * 64, p.K, n0, sB[st][sub]);
-            else lds_copy_slice<T, 4>(B, p.ldb, n0, p.N, kt * KW_BK + sub * 64, sB[st][sub]);
+            else lds_copy_slice<T, 4>(B, p.ldb, n0, nrows, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
     // blocks along K of W^T: a stage is T rows x 8 blocks; along N of [K][N]
@@ -1460,7 +1472,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         bbias = load_block_bias(p, n0 + (wave % NB) * 32);
         if (p.R && wave < NB * NB) {
             const bool vs = (p.ldc & 3) == 0 && hx_aligned8(p.C) && (p.ldr & 3) == 0 && hx_aligned8(p.R);
-            bres = load_block_res(p, m0 + (wave / NB) * 32 + (lane & 31), n0 + (wave % NB) * 32, lane, vs);
+            bres = load_block_res<NG>(p, m0 + (wave / NB) * 32 + (lane & 31), n0 + (wave % NB) * 32, lane, vs);
         }
     }
     f32x16 acc[NB][NB];   // [column block j][row block i]
@@ -1657,7 +1669,7 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         }
     }
     if (m >= p.M) return;
-    kw_store(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store, bbias, bres);
+    kw_store<NG>(p, m, n0 + (blk % NB) * 32, lane, sum, vec_store, bbias, bres);
 }
 
 // ---- W^T large-M path: big wave tiles, fragment reads under the MFMAs ----------
@@ -2344,6 +2356,13 @@ int kw_auto(int M, int N) {
     return t64 <= 256 ? 64 : 0;
 }
 
+// Within the 32-row K-across-waves choice: 32 x 24 tiles where 32 x 32 leaves
+// CUs of the round idle and 32 x 24 still fits it.
+bool kw24_auto(int M, int N) {
+    const long long rows = (M + 31) / 32, t32 = rows * ((N + 31) / 32), t24 = rows * ((N + 23) / 24);
+    return t32 < 256 && t24 <= 256 && t24 > t32;
+}
+
 // The large-tile kernel for tile bm x bn with a ring of `stages` slices;
 // false when that form is not built (the rope epilogue exists for the forms
 // the automatic choice uses).
@@ -2708,6 +2727,12 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         return;
     }
     if (kw == 32) {
+        const bool t24 = path == 4 ? g_ov_bn.load() == 24 : kw24_auto(p.M, p.N);
+        if (t24) {
+            HX_LAUNCH((gemm_nk_kw<32, false, false, 0, false, 24>),
+                      dim3((unsigned) ((p.N + 23) / 24), (unsigned) ((p.M + 31) / 32)), dim3(TPB), 0, p);
+            return;
+        }
         const dim3 grid((unsigned) ((p.N + 31) / 32), (unsigned) ((p.M + 31) / 32));
         HX_LAUNCH((gemm_nk_kw<32>), grid, dim3(TPB), 0, p);
         return;
@@ -2822,7 +2847,7 @@ extern "C" int hexlib_gpu_gemm_override(int bm, int bn, int splits, int path) {
                                    : (bm == 0 && bn == 0) || (bm == 256 && bn == 128) ||
                                          (bm == 128 && bn == 128) || (bm == 64 && bn == 64) ||
                                          (bm == 32 && bn == 64) || (bm == 64 && bn == 32) ||
-                                         (path == 3 && bm == 32 && bn == 32);
+                                         (path == 3 && bm == 32 && bn == 32) || (path == 4 && bm == 32 && bn == 24);
     if (!tile_ok || splits < 0 || splits > MAX_SPLITS || path < 0 || path > 7 || path == 6 ||
         (path == 7 && (bm || bn || (splits && splits != 4 && splits != 8 && splits != 16))) ||
         (path == 5 && splits > 3))

@@ -381,7 +381,8 @@ const char *hexlib_gpu_status_name(int status);
  * (0 = heuristic, at most 16) and W^T code path (0 = automatic,
  * 1 = register-staged, 2 = direct-to-LDS, 3 = the small-M register-operand
  * kernel with tile 32x32 or 32x64, 4 = the K-across-waves kernel for
- * K % 256 == 0 (tile 64x64 selects its 64x64 form, else 32x32), 5 = the
+ * K % 256 == 0 (tile 64x64 selects its 64x64 form, 32x24 its 32-row form
+ * with 24-column tiles on a plain fp16 W^T, else 32x32), 5 = the
  * large-tile kernel with bm in {128, 256} and bn in {128, 192, 256}, where
  * `splits` is its ring depth instead (0 = 2, at most 3; a form not built falls
  * back to the automatic choice), 7 = the 16-row MFMA kernel for K-grouped

@@ -249,7 +249,8 @@ def test_forced_split_batched_matmul(dev, splits):
 def test_override_rejects_bad_values(dev):
     for args in [(32, 32, 0, 0), (64, 64, 17, 0), (64, 64, -1, 0), (64, 64, 0, 6), (256, 256, 0, 0),
                  (32, 128, 0, 3), (128, 32, 0, 3), (64, 64, 0, 5), (256, 256, 4, 5), (192, 256, 0, 5),
-                 (64, 64, 0, 7), (0, 0, 2, 7), (0, 0, 12, 7), (0, 0, 0, 6), (0, 0, 0, 8)]:
+                 (64, 64, 0, 7), (0, 0, 2, 7), (0, 0, 12, 7), (0, 0, 0, 6), (0, 0, 0, 8),
+                 (32, 24, 0, 3), (32, 24, 0, 5)]:
         assert dev.lib.hexlib_gpu_gemm_override(*args) != 1
     assert dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0) == 1
 
@@ -501,17 +502,22 @@ def test_q8k_is_the_f16_gemm_on_its_dequantized_weight(dev, M):
     np.testing.assert_array_equal(dev.down(do), exact)
 
 
-@pytest.mark.parametrize("tile", [32, 64])
+KW_TILES = {32: (0, 0), 64: (64, 64), 24: (32, 24)}
+
+
+@pytest.mark.parametrize("tile", [32, 64, 24])
 @pytest.mark.parametrize("M,Kd,N,act,resid", [(256, 3072, 768, 0, True), (256, 3072, 768, 1, False),
                                               (64, 3072, 3072, 1, False), (64, 3072, 1024, 0, False),
                                               (70, 2048, 40, 2, True), (1, 4096, 64, 0, False),
-                                              (300, 256, 136, 0, True), (33, 512, 100, 1, False)])
+                                              (300, 256, 136, 0, True), (33, 512, 100, 1, False),
+                                              (40, 256, 77, 1, True), (256, 768, 760, 0, True)])
 def test_kw_long_k_path(dev, tile, M, Kd, N, act, resid):
-    """The K-across-waves kernels (32x32 and 64x64 tiles, forced with path 4;
-    automatic where their workgroups fit one round): ragged M and N, every
-    activation, with and without the residual epilogue. Within the GEMM
-    tolerance of the oracle; the residual form bit-identical to the plain form
-    followed by add_fp16."""
+    """The K-across-waves kernels (32x32, 64x64 and 32x24 tiles, forced with
+    path 4; automatic where their workgroups fit one round): ragged M and N
+    (N = 77: no vector stores; 760 and 100: a 32x24 grid's last tile 16 and 4
+    columns wide), every activation, with and without the residual epilogue.
+    Within the GEMM tolerance of the oracle; the residual form bit-identical to
+    the plain form followed by add_fp16."""
     r = rng(15)
     a = h16(r.standard_normal((M, Kd)))
     w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
@@ -519,7 +525,7 @@ def test_kw_long_k_path(dev, tile, M, Kd, N, act, resid):
     res = h16(r.standard_normal((M, N)))
     da, dw, db, dr = dev.up(a), dev.up(np.ascontiguousarray(w.T)), dev.up(bias), dev.up(res)
     d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
-    assert dev.lib.hexlib_gpu_gemm_override(tile if tile == 64 else 0, tile if tile == 64 else 0, 0, 4) == 1
+    assert dev.lib.hexlib_gpu_gemm_override(*KW_TILES[tile], 0, 4) == 1
     try:
         dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
         if resid:
