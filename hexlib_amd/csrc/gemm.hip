@@ -1595,18 +1595,25 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         mma_stage(st);
     }
     }
-    // combine the waves' partial tiles: [wave][block][e/4][lane][4] floats over the ring
+    // combine the waves' partial tiles: [wave][block][e/4][lane][4] floats over
+    // the ring. The q8_0 forms keep each wave's partial of the block it
+    // stores (block `wave`) in registers and write only the others: same sum,
+    // same order (the batch-1 q8_0 plan 0.690 -> 0.677 ms; the q4_0 plan lost
+    // 0.6% and the fp16 plan 0.3% with it, so those forms write all four)
+    constexpr bool KEEP_OWN = QB == 8;
     HX_WAIT_VMCNT(0);
     __builtin_amdgcn_s_barrier();
     float *red = reinterpret_cast<float *>(&sA[0][0][0]);
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
+        for (int j = 0; j < NB; ++j) {
+            if (KEEP_OWN && i * NB + j == wave) continue;
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4)
                 *reinterpret_cast<f32x4 *>(red + (((wave * NB * NB + i * NB + j) * 4 + e4) * 64 + lane) * 4) =
                     f32x4{acc[j][i][4 * e4], acc[j][i][4 * e4 + 1], acc[j][i][4 * e4 + 2], acc[j][i][4 * e4 + 3]};
+        }
     // LNF: each lane's (sum x, sum x^2) pairs, [wave][row block][lane], in the
     // drained B ring (the partial tiles fill the A ring)
     float2 *lst = reinterpret_cast<float2 *>(&sB[0][0][0]);
@@ -1618,15 +1625,31 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     __builtin_amdgcn_s_barrier();
     if (wave >= NB * NB) return;
     const int blk = wave;                          // block (i, j) = (blk / NB, blk % NB)
+    f32x16 own{};
+    if constexpr (KEEP_OWN) {
+        own = acc[0][0];
+        if constexpr (NB == 2) {
+            if (blk == 1) own = acc[1][0];
+            else if (blk == 2) own = acc[0][1];
+            else if (blk == 3) own = acc[1][1];
+        }
+    }
+    // summed in wave order 0..3 from zero, the own partial in its place
     f32x16 sum = f32x16{};
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
+    for (int v = 0; v < 4; ++v) {
+        if (KEEP_OWN && v == blk) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sum[e] += own[e];
+            continue;
+        }
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
             const f32x4 t = *reinterpret_cast<const f32x4 *>(red + (((v * NB * NB + blk) * 4 + e4) * 64 + lane) * 4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) sum[4 * e4 + e] += t[e];
         }
+    }
     // lane l holds output row l % 32 of the block, columns 8 g + 4 (l / 32) .. + 3
     const int m = m0 + (blk / NB) * 32 + r;
     if constexpr (LNF) {
