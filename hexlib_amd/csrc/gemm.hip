@@ -773,6 +773,36 @@ __device__ __forceinline__ f16x8 kn_frag(const f16 *bs, int ncol, int q, int lan
     return __builtin_bit_cast(f16x8, (v8i16){h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]});
 }
 
+// The 32-column [K][N] sub-slice of the K-across-waves kernel: 64 k rows of
+// 32 halves (64 B), unswizzled. One wave-instruction copies 16 rows (four
+// lanes a row, 16 B each, landing contiguously as global_load_lds_dwordx4
+// places them); the four waves take 16 rows each. Rows k0 .. k0 + 63 and
+// columns n0 .. n0 + 31 must lie inside the weight (K % 256 == 0, N % 32 == 0).
+constexpr int KN32_ROW = 32;
+
+__device__ __forceinline__ void lds_copy_kn32(const f16 *__restrict__ base, long long ld, int k0, int n0, f16 *lds) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = wave * 16 + (lane >> 2);
+    const f16 *src = base + (long long) (k0 + r) * ld + n0 + (lane & 3) * 8;
+    const uint32_t dst = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) f16 *) (lds + wave * 16 * KN32_ROW);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(dst))
+                 : "memory", "m0");
+}
+
+// kn_frag's fragment (columns 0 .. 31, k step q) from that 32-column layout.
+__device__ __forceinline__ f16x8 kn32_frag(const f16 *bs, int q, int lane) {
+    const int nn = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int k0 = 16 * q + 8 * (lane >> 5) + ((lane & 15) >> 2);
+    v4i16 h[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        h[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16 *) (bs + (k0 + 4 * u) * KN32_ROW + nn));
+    return __builtin_bit_cast(f16x8, (v8i16){h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]});
+}
+
 // WM x WN waves; each owns a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles.
 // LN: A's row block is loaded whole, layer-normalised in LDS, and only B
 // streams through the ring (BM = 64, K <= 64 * LN_KT, 512 <= K).
@@ -1337,8 +1367,9 @@ __device__ __forceinline__ void load_block_c1(const GemmArgs &p, int nb, int lan
 // T x T tile (T = 32: one 32x32 block, 3 stages; T = 64: 2x2 blocks per wave,
 // 2 stages -- 128 KB of LDS). With T = 64 wave w stores block w after the
 // reduction; with T = 32 wave 0 stores.
-// KN: the weight is [K][N] (N % 64 == 0, T = 64): each sub-slice is its
-// [64 k][64 n] tile as stored, read through kn_frag.
+// KN: the weight is [K][N]: with T = 64 (N % 64 == 0) each sub-slice is its
+// [64 k][64 n] tile as stored, read through kn_frag; with T = 32 (N % 32 == 0)
+// its [64 k][32 n] tile, through kn32_frag.
 // QB: the weight is block-quantized W^T, [N][K/32] blocks of an fp16 scale
 // and 32 codes, 2-byte aligned -- QB = 8: q8_0 (32 int8, 34 bytes), QB = 4:
 // q4_0 grouped along K (16 bytes of nibbles, 18 bytes). Each stage's blocks are
@@ -1361,7 +1392,7 @@ __device__ __forceinline__ void load_block_c1(const GemmArgs &p, int nb, int lan
 // a round of 256 with 12.5% fewer bytes per workgroup.
 template <int T, bool ROPE = false, bool KN = false, int QB = 0, bool LNF = false, int TN = T>
 __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
-    static_assert(!KN || (T == 64 && !ROPE), "the [K][N] weight comes in 64-column tiles");
+    static_assert(!KN || !ROPE, "no rope epilogue on the [K][N] weight");
     static_assert(QB == 0 || ((QB == 8 || QB == 4) && (!KN || QB == 4) && (!ROPE || (QB == 8 && !KN))),
                   "quantized weights: q8_0 / q4_0 blocks along K of W^T, or q4_0 blocks along N of [K][N]; "
                   "the rope epilogue with q8_0 blocks along K (rows pair-interleaved like the fp16 W^T)");
@@ -1376,8 +1407,10 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
     constexpr int LOADS = 4 * 2 * (T / 32);     // wave-instructions per stage: 4 sub-slices x (A + B) x T/32
     static_assert(LOADS * (STAGES - 1) <= 63, "vmcnt holds at most 63");
     static_assert(STAGES * 4 * 2 * T * DS_ROW * 2 >= 4 * NB * NB * 16 * 64 * 4, "reduction fits in the ring");
+    // a [K][N] sub-slice is 64 k rows: of 64 columns (T = 64) or 32 (T = 32)
+    constexpr int SB = KN ? 64 * (T == 64 ? DS_ROW : KN32_ROW) : T * DS_ROW;
     __shared__ __attribute__((aligned(16))) f16 sA[STAGES][4][T * DS_ROW];
-    __shared__ __attribute__((aligned(16))) f16 sB[STAGES][4][T * DS_ROW];
+    __shared__ __attribute__((aligned(16))) f16 sB[STAGES][4][SB];
     const f16 *A = p.A;
     const f16 *B = reinterpret_cast<const f16 *>(p.B);
     const int m0 = blockIdx.y * T, n0 = blockIdx.x * TN;
@@ -1390,12 +1423,13 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
         for (int sub = 0; sub < 4; ++sub) {
             lds_copy_slice<T, 4>(A, p.lda, m0, p.M, kt * KW_BK + sub * 64, sA[st][sub]);
             if constexpr (Q8) continue;
+            else if constexpr (KN && T == 32) lds_copy_kn32(B, p.ldb, kt * KW_BK + sub * 64, n0, sB[st][sub]);
             else if constexpr (KN) lds_copy_slice<64, 4>(B, p.ldb, kt * KW_BK + sub * 64, p.K, n0, sB[st][sub]);
             else lds_copy_slice<T, 4>(B, p.ldb, n0, nrows, kt * KW_BK + sub * 64, sB[st][sub]);
         }
     };
     // blocks along K of W^T: a stage is T rows x 8 blocks; along N of [K][N]
-    // (KN, T = 64): 256 k x 2 blocks. Thread t takes blocks t + 256 u.
+    // (KN): 256 k x T / 32 blocks. Thread t takes blocks t + 256 u.
     constexpr int NQ = Q8 ? T * 8 / TPB : 1;
     struct Q8Regs {
         float d[NQ];
@@ -1406,6 +1440,10 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
+            if constexpr (KN && T == 32) {   // block (k, n0 / 32), k = kt * 256 + b
+                load_q4_block(Bq + (long long) (kt * KW_BK + b) * p.ldb + (n0 / 32) * 18, q.d[u], q.qs[u]);
+                continue;
+            }
             if constexpr (KN) {   // block (k, n0 / 32 + (b & 1)), k = kt * 256 + b / 2
                 load_q4_block(Bq + (long long) (kt * KW_BK + (b >> 1)) * p.ldb + (n0 / 32 + (b & 1)) * 18, q.d[u],
                               q.qs[u]);
@@ -1425,6 +1463,18 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
             const int b = threadIdx.x + TPB * u, row = b >> 3, kb = b & 7;
+            if constexpr (KN && T == 32) {
+                // the block's 32 values are row k = b of the 32-column sub-slice b / 64
+                f16 *drow = sB[st][b >> 6] + (b & 63) * KN32_ROW;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    f16x8 v;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = q4_val(q.d[u], nib(q.qs[u], (c * 8 + j) & 15, ((c * 8 + j) >> 4) * 4));
+                    *reinterpret_cast<f16x8 *>(drow + c * 8) = v;
+                }
+                continue;
+            }
             if constexpr (KN) {
                 // the block's 32 values are n = n0 + 32 (b & 1) + j of row k:
                 // four 8-column chunks of that k row of the [64 k][64 n] sub-slice
@@ -1504,7 +1554,8 @@ __global__ __launch_bounds__(TPB) void gemm_nk_kw(GemmArgs p) {
 #pragma unroll
             for (int h = 0; h < NB; ++h) {
                 const int rr = h * 32 + r;
-                if constexpr (KN) wf[h] = kn_frag(bs, h * 32, q, lane);
+                if constexpr (KN && T == 32) wf[h] = kn32_frag(bs, q, lane);
+                else if constexpr (KN) wf[h] = kn_frag(bs, h * 32, q, lane);
                 else wf[h] = *reinterpret_cast<const f16x8 *>(bs + rr * DS_ROW + ((c ^ swz(rr)) << 3));
                 xf[h] = *reinterpret_cast<const f16x8 *>(as + rr * DS_ROW + ((c ^ swz(rr)) << 3));
             }
@@ -2379,6 +2430,16 @@ int kw_auto(int M, int N) {
     return t64 <= 256 ? 64 : 0;
 }
 
+// The [K][N] K-across-waves tile (fp16 or N-blocked q4_0; N % 32 == 0): 64
+// (N % 64 == 0) or 32 as kw_auto picks, or forced with path 4 (tile 64x64:
+// the 64-column form, else the 32-column one); 0 for neither.
+int kw_kn_tile(int path, int M, int N) {
+    if (path == 4) return g_ov_bm.load() == 64 ? (N % 64 == 0 ? 64 : 0) : 32;
+    if (path != 0) return 0;
+    const int t = kw_auto(M, N);
+    return t == 64 && N % 64 == 0 ? 64 : t == 32 ? 32 : 0;
+}
+
 // Within the 32-row K-across-waves choice: 32 x 24 tiles where 32 x 32 leaves
 // CUs of the round idle and 32 x 24 still fits it.
 bool kw24_auto(int M, int N) {
@@ -2636,17 +2697,22 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         const int stages = path == 5 && g_ov_splits.load() ? g_ov_splits.load() : 2;
         if (bt.bm && launch_big(p, bt, stages)) return;
     }
-    // the [K][N] weight at few rows: the 64x64 K-across-waves form, where the
-    // W^T rule picks that tile (256 x 768 x 2304: 8.1 us against 9.5 on the
-    // tiled ring); where it picks 32x32 (K = 3072, N = 768) the tiled ring is
-    // faster (12.6 us against 15.3), and so, at 256 x 768 x 768, is this form
-    // (7.6 against 9.1) with no 32-column [K][N] tile
-    const bool kw_kn_ok = MODE == B_KN && batch == 1 && p.K % KW_BK == 0 && p.N % 64 == 0 && p.lda % 8 == 0 &&
-                          p.ldb % 8 == 0 && avec && bvec && (p.M + 63) / 64 <= 65535;
-    const int kw_kn_auto = kw_auto(p.M, p.N);
-    if (kw_kn_ok && (path == 4 || (path == 0 && (kw_kn_auto == 64 || (kw_kn_auto == 32 && p.K <= 768))))) {
+    // the [K][N] weight at few rows: the K-across-waves kernel's [K][N] forms
+    // with the tile the W^T rule picks -- 64x64 (256 x 768 x 2304: 5.6 us
+    // against 7.4 on the tiled ring) or the 32-column tile where it picks 32x32
+    // (N % 32 == 0; 256 x 3072 x 768 8.9 us against 12.1 tiled and 13.1 on
+    // the 64x64 form, 256 x 768 x 768 4.1 against 5.5 on the 64x64 form)
+    const bool kw_kn_ok = MODE == B_KN && batch == 1 && p.K % KW_BK == 0 && p.N % 32 == 0 && p.lda % 8 == 0 &&
+                          p.ldb % 8 == 0 && avec && bvec && (p.M + 31) / 32 <= 65535;
+    const int kw_kn = kw_kn_ok ? kw_kn_tile(path, p.M, p.N) : 0;
+    if (kw_kn == 64) {
         const dim3 grid((unsigned) ((p.N + 63) / 64), (unsigned) ((p.M + 63) / 64));
         HX_LAUNCH((gemm_nk_kw<64, false, true>), grid, dim3(TPB), 0, p);
+        return;
+    }
+    if (kw_kn == 32) {
+        HX_LAUNCH((gemm_nk_kw<32, false, true>), dim3((unsigned) (p.N / 32), (unsigned) ((p.M + 31) / 32)), dim3(TPB),
+                  0, p);
         return;
     }
     // q8_0 and K-grouped q4_0 weights at few rows: the K-across-waves kernel
@@ -2710,16 +2776,21 @@ void launch(GemmArgs p, int batch, bool avec, bool bvec) {
         }
     }
     // q4_0 blocked along N (the reference ABI, [K][N/32] blocks) at few rows: the
-    // 64x64 K-across-waves kernel in its [K][N] form, each stage's blocks
-    // dequantized into the ring in the layout its fp16 copies fill. Where the
-    // 32x32 tile would be the choice (N = 768) only up to K = 768, as for the
-    // fp16 [K][N] weight: 256 x 768 x 768 9.8 us against 14.1 on the
-    // register-staged kernel, 256 x 3072 x 768 25.2 against 18.6.
-    const bool kw_q4n_ok = MODE == B_Q4N && batch == 1 && p.K % KW_BK == 0 && p.N % 64 == 0 && p.lda % 8 == 0 &&
-                           avec && (p.M + 63) / 64 <= 65535 && !p.rcos && !p.ln_w && path != 1;
-    const int kw_q4n_auto = kw_auto(p.M, p.N);
-    if (kw_q4n_ok && (path == 4 || (path == 0 && (kw_q4n_auto == 64 || (kw_q4n_auto == 32 && p.K <= 768))))) {
+    // K-across-waves kernel's [K][N] forms, each stage's blocks dequantized into
+    // the ring in the layout its fp16 copies fill, with the fp16 rule's tile:
+    // 256 x 3072 x 768 13.9 us on the 32-column tile against 17.3 on the
+    // register-staged kernel and 23.7 on the 64x64 form; 256 x 768 x 768 5.6
+    // against 8.0 (64x64) and 13.3.
+    const bool kw_q4n_ok = MODE == B_Q4N && batch == 1 && p.K % KW_BK == 0 && p.N % 32 == 0 && p.lda % 8 == 0 &&
+                           avec && (p.M + 31) / 32 <= 65535 && !p.rcos && !p.ln_w && path != 1;
+    const int kw_q4n = kw_q4n_ok ? kw_kn_tile(path, p.M, p.N) : 0;
+    if (kw_q4n == 64) {
         HX_LAUNCH((gemm_nk_kw<64, false, true, 4>), dim3((unsigned) (p.N / 64), (unsigned) ((p.M + 63) / 64)),
+                  dim3(TPB), 0, p);
+        return;
+    }
+    if (kw_q4n == 32) {
+        HX_LAUNCH((gemm_nk_kw<32, false, true, 4>), dim3((unsigned) (p.N / 32), (unsigned) ((p.M + 31) / 32)),
                   dim3(TPB), 0, p);
         return;
     }

@@ -72,19 +72,21 @@ def test_matmul_epilogue_q4_nblocked(dev, M, Kd, N, act):
 
 
 @pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 2304, 0), (256, 768, 768, 1), (256, 768, 3072, 1),
-                                        (70, 512, 128, 2), (1, 256, 64, 0), (300, 1024, 192, 0)])
+                                        (70, 512, 128, 2), (1, 256, 64, 0), (300, 1024, 192, 0),
+                                        (256, 3072, 768, 0), (64, 3072, 1024, 2)])
 def test_q4_nblocked_kw_path(dev, M, Kd, N, act):
     """The reference-ABI q4_0 weight (blocks along N) on the K-across-waves
-    kernel's [K][N] form (override path 4, and the automatic route at these
-    shapes) is bit-identical to the same kernel's fp16 [K][N] form on the
-    dequantized weight, and within the epilogue tolerance of the oracle and of
+    kernel's [K][N] forms (override path 4 with tile 64x64 and with the
+    32-column tile, and the automatic route at these shapes) is bit-identical
+    to the same kernel's fp16 [K][N] form on the dequantized weight, and within the epilogue tolerance of the oracle and of
     the register-staged kernel (path 1)."""
     a, w, bias = _q4_inputs(M, Kd, N, 17)
     wq = pack_q4_0_nblocked(w)
     wd = h16(dequantize_q4_0_fp16(wq, (Kd, N)))
     da, dw, db, dwd = dev.up(a), dev.up(np.frombuffer(wq, np.uint8)), dev.up(bias), dev.up(wd)
     outs = []
-    for ov, dense in (((64, 64, 0, 4), False), ((0, 0, 0, 0), False), ((0, 0, 1, 1), False), ((64, 64, 0, 4), True)):
+    for ov, dense in (((64, 64, 0, 4), False), ((0, 0, 0, 0), False), ((0, 0, 1, 1), False), ((64, 64, 0, 4), True),
+                      ((0, 0, 0, 4), False), ((0, 0, 0, 4), True)):
         do = dev.empty((M, N), np.float16)
         assert dev.lib.hexlib_gpu_gemm_override(*ov) == 1
         try:
@@ -98,6 +100,9 @@ def test_q4_nblocked_kw_path(dev, M, Kd, N, act):
         outs.append(dev.down(do))
     np.testing.assert_array_equal(outs[0].view(np.uint16), outs[3].view(np.uint16))
     np.testing.assert_array_equal(outs[1].view(np.uint16), outs[3].view(np.uint16))
+    # the 32-column form: the same sums in the same order as the 64-column one
+    np.testing.assert_array_equal(outs[4].view(np.uint16), outs[5].view(np.uint16))
+    np.testing.assert_array_equal(outs[4].view(np.uint16), outs[3].view(np.uint16))
     want = K.matmul_epilogue_fp16(a, wq, bias, Kd, N, act)
     assert K.close_f16(outs[0], want, 0.01, 3e-4).all()
     assert K.close_f16(outs[2], want, 0.01, 3e-4).all()
@@ -699,18 +704,21 @@ def test_batched_matmul_kn_direct_matches_register_path(dev, dims):
         assert K.close_f16(o, want, 1e-2, 1e-3).all()
 
 
-@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 2304, 1), (256, 768, 768, 0), (200, 512, 192, 2), (256, 3072, 768, 0)])
-def test_kn_weight_kw_path(dev, M, Kd, N, act):
-    """matmul_epilogue_f16w on the 64x64 K-across-waves kernel (path 4 with
-    tile 64x64; K % 256 == 0, N % 64 == 0): bit-identical to the W^T form of
-    the same kernel, and within the harness tolerance of the oracle."""
+@pytest.mark.parametrize("tile", [64, 32])
+@pytest.mark.parametrize("M,Kd,N,act", [(256, 768, 2304, 1), (256, 768, 768, 0), (200, 512, 192, 2), (256, 3072, 768, 0),
+                                        (33, 512, 96, 1), (64, 3072, 1024, 2)])
+def test_kn_weight_kw_path(dev, tile, M, Kd, N, act):
+    """matmul_epilogue_f16w on the K-across-waves kernel's [K][N] forms (path 4;
+    K % 256 == 0): tile 64x64 (N % 64 == 0; else another path) and the
+    32-column tile (N % 32 == 0), each bit-identical to the W^T form of the
+    same tile, and within the harness tolerance of the oracle."""
     r = rng(26)
     a = h16(r.standard_normal((M, Kd)))
     w = h16(r.standard_normal((Kd, N)) / np.sqrt(Kd))
     bias = (0.02 * r.standard_normal(N)).astype(np.float32)
     da, dw, dwt, db = dev.up(a), dev.up(w), dev.up(np.ascontiguousarray(w.T)), dev.up(bias)
     d1, d2 = dev.empty((M, N), np.float16), dev.empty((M, N), np.float16)
-    assert dev.lib.hexlib_gpu_gemm_override(64, 64, 0, 4) == 1
+    assert dev.lib.hexlib_gpu_gemm_override(tile if tile == 64 else 0, tile if tile == 64 else 0, 0, 4) == 1
     try:
         dev.lib.matmul_epilogue_f16w_fp16(dev.ptr(da), dev.ptr(dw), dev.ptr(db), dev.ptr(d1), M, Kd, N, act)
         dev.lib.matmul_epilogue_f16wt_fp16(dev.ptr(da), dev.ptr(dwt), dev.ptr(db), dev.ptr(d2), M, Kd, N, act)
@@ -718,7 +726,8 @@ def test_kn_weight_kw_path(dev, M, Kd, N, act):
     finally:
         dev.lib.hexlib_gpu_gemm_override(0, 0, 0, 0)
     got = dev.down(d1)
-    np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
+    if tile == 32 or N % 64 == 0:
+        np.testing.assert_array_equal(got.view(np.uint16), dev.down(d2).view(np.uint16))
     assert K.close_f16(got, K.matmul_epilogue_f16w(a, w, bias, act), 1e-2, 1e-3).all()
 
 
